@@ -1,0 +1,857 @@
+// Host orchestration of the encoder forward and the C ABI (include/bark_hip.h).
+//
+// Mirrors the reference's GPU encoder driver (src/encoder.rs:412-830 load,
+// :1985-2657 encode/encode_pre) and conv front end (src/sub_gpu.rs:574-776),
+// re-planned for one MI355X:
+//  - weights live in HBM in their compact form (f16 or 4-bit codes + 16-entry
+//    f16 tables), fused and permuted once at finalize;
+//  - a forward over one or several utterances packs their frames into one row
+//    space (each utterance 64-row aligned), so every linear streams its weights
+//    once per call whatever the batch;
+//  - per block: 4 LayerNorm launches (norm_out fused with the next block's
+//    first norm), 9 GEMMs with fused epilogues, 1 attention, 1 dwconv.
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "../../include/bark_hip.h"
+#include "kernels.h"
+
+namespace bark {
+namespace {
+
+thread_local std::string g_last_error;
+
+inline int conv_len(int l) { return (l + 2 - 3) / 2 + 1; }  // src/sub.rs:11-13
+
+inline uint16_t f32_to_f16_bits(float v) {
+  const half h = (half)v;  // IEEE round-to-nearest-even
+  uint16_t b;
+  std::memcpy(&b, &h, 2);
+  return b;
+}
+inline float f16_bits_to_f32(uint16_t b) {
+  half h;
+  std::memcpy(&h, &b, 2);
+  return (float)h;
+}
+
+// src/bark.rs:597-611
+float expand_level(uint32_t code, uint32_t k, const uint16_t* levels) {
+  if (code == 0) return 0.0f;
+  const bool negative = code > k;
+  const uint32_t mag = negative ? code - k - 1 : code - 1;
+  const float value = mag < k ? f16_bits_to_f32(levels[mag]) : 0.0f;
+  return negative ? -value : value;
+}
+
+struct HostTensor {
+  enum Kind { F32, F16, LUT4 } kind = F32;
+  std::vector<int64_t> shape;
+  std::vector<float> f32;
+  std::vector<uint16_t> f16;
+  std::vector<uint8_t> codes;  // rows x cols/2
+  std::vector<uint16_t> lut;   // rows x 16
+  int64_t rows = 0, cols = 0;
+  int64_t numel() const {
+    int64_t n = 1;
+    for (auto s : shape) n *= s;
+    return n;
+  }
+};
+
+// A linear weight on the host side of finalize: f16 bits or codes + tables.
+struct HostLinear {
+  bool lut4 = false;
+  int rows = 0, cols = 0;
+  std::vector<uint16_t> w16;
+  std::vector<uint8_t> codes;
+  std::vector<uint16_t> lut;
+};
+
+struct DevLayer {
+  GemmWeight qkv, relk, o, ff1a, ff1b, ff2a, ff2b, pw1, pw2;
+  float *dw = nullptr, *bn_a = nullptr, *bn_b = nullptr, *bu = nullptr, *bv = nullptr;
+  float* ln_w[5] = {};
+  float* ln_b[5] = {};
+};
+
+// Grow-only device buffer; contents are zeroed whenever it is (re)allocated.
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  template <class T>
+  T* as() const {
+    return static_cast<T*>(p);
+  }
+};
+
+struct SeqPlan {
+  int frames = 0, valid = 0;
+  int t = 0;      // encoder frames
+  int start = 0;  // first row in the packed row space
+};
+
+}  // namespace
+}  // namespace bark
+
+using namespace bark;
+
+struct BarkHip {
+  int device = 0;
+  int n_layers = 24;
+  hipStream_t stream = nullptr;
+  std::mutex mu;
+  std::map<std::string, HostTensor> staged;
+  bool finalized = false;
+  bool has_front_end = false;
+
+  std::vector<void*> allocs;  // weights, freed at destroy
+  GemmWeight sub_w, proj_w, sub_pw1, sub_pw2;
+  float *sub_b = nullptr, *proj_b = nullptr;
+  float *l0w = nullptr, *l0b = nullptr, *l2w = nullptr, *l2b = nullptr, *l3b = nullptr;
+  float *l5w = nullptr, *l5b = nullptr, *l6b = nullptr;
+  std::vector<DevLayer> layers;
+
+  // position table rows for pos = pos_t-1 .. -(pos_t-1), f16, plus zero rows
+  DevBuf pos;
+  int pos_t = 0;
+
+  // workspace
+  DevBuf sub16, xn, hid, qu, qv, kh, vt, rk, ao, h, h2, glu, pooler, dump, bounds, tiles;
+  DevBuf y1, y2, y3, y4, mel, subf32;
+
+  template <class T>
+  T* upload(const T* src, size_t n) {
+    void* p = nullptr;
+    BARK_HIP_CHECK(hipMalloc(&p, std::max<size_t>(n, 1) * sizeof(T)));
+    allocs.push_back(p);
+    BARK_HIP_CHECK(hipMemcpy(p, src, n * sizeof(T), hipMemcpyHostToDevice));
+    return static_cast<T*>(p);
+  }
+
+  void ensure(DevBuf& b, size_t bytes) {
+    if (bytes <= b.cap) return;
+    BARK_HIP_CHECK(hipStreamSynchronize(stream));
+    if (b.p) BARK_HIP_CHECK(hipFree(b.p));
+    b.p = nullptr;
+    b.cap = 0;
+    const size_t want = (bytes + 4095) & ~size_t(4095);
+    BARK_HIP_CHECK(hipMalloc(&b.p, want));
+    BARK_HIP_CHECK(hipMemset(b.p, 0, want));
+    b.cap = want;
+  }
+
+  ~BarkHip() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (void* p : allocs) (void)hipFree(p);
+    DevBuf* bufs[] = {&pos, &sub16, &xn, &hid, &qu, &qv, &kh, &vt, &rk, &ao, &h, &h2, &glu,
+                      &pooler, &dump, &bounds, &tiles, &y1, &y2, &y3, &y4, &mel, &subf32};
+    for (DevBuf* b : bufs)
+      if (b->p) (void)hipFree(b->p);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  // ------------------------------------------------------------ finalize --
+  const HostTensor& need(const std::string& name) {
+    auto it = staged.find(name);
+    BARK_REQUIRE(it != staged.end(), "missing tensor " + name);
+    return it->second;
+  }
+
+  std::vector<float> vec_f32(const std::string& name, int64_t n) {
+    const HostTensor& t = need(name);
+    std::vector<float> out;
+    if (t.kind == HostTensor::F32) {
+      out = t.f32;
+    } else if (t.kind == HostTensor::F16) {
+      out.resize(t.f16.size());
+      for (size_t i = 0; i < t.f16.size(); ++i) out[i] = f16_bits_to_f32(t.f16[i]);
+    } else {
+      throw Error{name + ": a 4-bit tensor where f32 values are expected"};
+    }
+    BARK_REQUIRE((int64_t)out.size() == n,
+                 name + ": expected " + std::to_string(n) + " values, got " +
+                     std::to_string(out.size()));
+    return out;
+  }
+
+  HostLinear linear(const std::string& name, int rows, int cols, bool allow_lut4) {
+    const HostTensor& t = need(name);
+    HostLinear L;
+    L.rows = rows;
+    L.cols = cols;
+    if (t.kind == HostTensor::LUT4) {
+      BARK_REQUIRE(allow_lut4, name + ": 4-bit storage is not supported for this tensor");
+      BARK_REQUIRE(t.rows == rows && t.cols == cols, name + ": 4-bit tensor has a wrong shape");
+      L.lut4 = true;
+      L.codes = t.codes;
+      L.lut = t.lut;
+      return L;
+    }
+    const int64_t n = (int64_t)rows * cols;
+    if (t.kind == HostTensor::F16) {
+      BARK_REQUIRE((int64_t)t.f16.size() == n, name + ": wrong element count");
+      L.w16 = t.f16;
+    } else {
+      BARK_REQUIRE((int64_t)t.f32.size() == n, name + ": wrong element count");
+      L.w16.resize(n);
+      for (int64_t i = 0; i < n; ++i) L.w16[i] = f32_to_f16_bits(t.f32[i]);
+    }
+    return L;
+  }
+
+  GemmWeight to_device(const HostLinear& L) {
+    GemmWeight g;
+    g.n = L.rows;
+    g.k = L.cols;
+    if (L.lut4) {
+      g.codes = upload(L.codes.data(), L.codes.size());
+      g.lut = reinterpret_cast<const half*>(upload(L.lut.data(), L.lut.size()));
+    } else {
+      g.w16 = reinterpret_cast<const half*>(upload(L.w16.data(), L.w16.size()));
+    }
+    return g;
+  }
+
+  // Rows of several linears stacked (q|k|v, src/encoder.rs:342-402).
+  static HostLinear stack(const std::vector<HostLinear>& parts, const std::string& what) {
+    HostLinear out;
+    out.lut4 = parts[0].lut4;
+    out.cols = parts[0].cols;
+    for (const auto& p : parts) {
+      BARK_REQUIRE(p.lut4 == out.lut4, what + " mixes 4-bit and f16 storage");
+      BARK_REQUIRE(p.cols == out.cols, what + ": column mismatch");
+      out.rows += p.rows;
+      out.w16.insert(out.w16.end(), p.w16.begin(), p.w16.end());
+      out.codes.insert(out.codes.end(), p.codes.begin(), p.codes.end());
+      out.lut.insert(out.lut.end(), p.lut.begin(), p.lut.end());
+    }
+    return out;
+  }
+
+  // pw1 rows (2048) reordered so each 64-row group is [value 32 | gate 32] of
+  // the same 32 output channels: new row 64g+32s+j <- old row 1024s+32g+j.
+  static HostLinear interleave_glu(const HostLinear& in) {
+    HostLinear out = in;
+    const int half_rows = in.rows / 2;
+    auto src_row = [&](int nr) {
+      const int g = nr / 64, s = (nr % 64) / 32, j = nr % 32;
+      return s * half_rows + 32 * g + j;
+    };
+    for (int nr = 0; nr < in.rows; ++nr) {
+      const int orow = src_row(nr);
+      if (in.lut4) {
+        const size_t cb = in.cols / 2;
+        std::memcpy(&out.codes[nr * cb], &in.codes[orow * cb], cb);
+        std::memcpy(&out.lut[nr * 16], &in.lut[orow * 16], 32);
+      } else {
+        std::memcpy(&out.w16[(size_t)nr * in.cols], &in.w16[(size_t)orow * in.cols],
+                    (size_t)in.cols * 2);
+      }
+    }
+    return out;
+  }
+
+  float* f32_dev(const std::string& name, int64_t n) {
+    auto v = vec_f32(name, n);
+    return upload(v.data(), v.size());
+  }
+
+  void finalize() {
+    BARK_REQUIRE(!finalized, "finalize called twice");
+    sub_w = to_device(linear("encoder.subsampling.linear.weight", 1024, 4096, true));
+    sub_b = f32_dev("encoder.subsampling.linear.bias", 1024);
+    proj_w = to_device(linear("encoder_projector.weight", PROJ, HIDDEN, false));
+    proj_b = f32_dev("encoder_projector.bias", PROJ);
+    layers.resize(n_layers);
+    for (int l = 0; l < n_layers; ++l) {
+      const std::string p = "encoder.layers." + std::to_string(l) + ".";
+      DevLayer& L = layers[l];
+      L.qkv = to_device(stack({linear(p + "self_attn.q_proj.weight", 1024, 1024, true),
+                               linear(p + "self_attn.k_proj.weight", 1024, 1024, true),
+                               linear(p + "self_attn.v_proj.weight", 1024, 1024, true)},
+                              "fused q/k/v"));
+      L.relk = to_device(linear(p + "self_attn.relative_k_proj.weight", 1024, 1024, true));
+      L.o = to_device(linear(p + "self_attn.o_proj.weight", 1024, 1024, true));
+      L.ff1a = to_device(linear(p + "feed_forward1.linear1.weight", 4096, 1024, true));
+      L.ff1b = to_device(linear(p + "feed_forward1.linear2.weight", 1024, 4096, true));
+      L.ff2a = to_device(linear(p + "feed_forward2.linear1.weight", 4096, 1024, true));
+      L.ff2b = to_device(linear(p + "feed_forward2.linear2.weight", 1024, 4096, true));
+      L.pw1 = to_device(interleave_glu(linear(p + "conv.pointwise_conv1.weight", 2048, 1024, true)));
+      L.pw2 = to_device(linear(p + "conv.pointwise_conv2.weight", 1024, 1024, true));
+      {  // depthwise weights as f16-rounded values (the reference stores f16)
+        auto dw = vec_f32(p + "conv.depthwise_conv.weight", 1024 * 9);
+        for (auto& v : dw) v = f16_bits_to_f32(f32_to_f16_bits(v));
+        L.dw = upload(dw.data(), dw.size());
+      }
+      {  // BatchNorm fold a = w/sqrt(var+1e-5), b = bias - mean*a (src/encoder.rs:546-557)
+        auto w = vec_f32(p + "conv.norm.weight", 1024), b = vec_f32(p + "conv.norm.bias", 1024);
+        auto m = vec_f32(p + "conv.norm.running_mean", 1024);
+        auto v = vec_f32(p + "conv.norm.running_var", 1024);
+        std::vector<float> a(1024), bb(1024);
+        for (int c = 0; c < 1024; ++c) {
+          a[c] = w[c] / std::sqrt(v[c] + 1e-5f);
+          bb[c] = b[c] - m[c] * a[c];
+        }
+        L.bn_a = upload(a.data(), a.size());
+        L.bn_b = upload(bb.data(), bb.size());
+      }
+      const char* ln_names[5] = {"norm_feed_forward1", "norm_self_att", "norm_conv",
+                                 "norm_feed_forward2", "norm_out"};
+      for (int i = 0; i < 5; ++i) {
+        L.ln_w[i] = f32_dev(p + ln_names[i] + ".weight", 1024);
+        L.ln_b[i] = f32_dev(p + ln_names[i] + ".bias", 1024);
+      }
+      L.bu = f32_dev(p + "self_attn.bias_u", 1024);
+      L.bv = f32_dev(p + "self_attn.bias_v", 1024);
+    }
+    // conv front end (optional: encode_sub does not need it)
+    const std::string s = "encoder.subsampling.layers.";
+    has_front_end = staged.count(s + "0.weight") > 0;
+    if (has_front_end) {
+      l0w = f32_dev(s + "0.weight", 256 * 9);
+      l0b = f32_dev(s + "0.bias", 256);
+      l2w = f32_dev(s + "2.weight", 256 * 9);
+      l2b = f32_dev(s + "2.bias", 256);
+      sub_pw1 = to_device(linear(s + "3.weight", 256, 256, false));
+      l3b = f32_dev(s + "3.bias", 256);
+      l5w = f32_dev(s + "5.weight", 256 * 9);
+      l5b = f32_dev(s + "5.bias", 256);
+      sub_pw2 = to_device(linear(s + "6.weight", 256, 256, false));
+      l6b = f32_dev(s + "6.bias", 256);
+    }
+    staged.clear();
+    finalized = true;
+  }
+
+  // ------------------------------------------------------- position table --
+  // src/encoder.rs:228-245 evaluated on the host with the platform libm, as
+  // the reference does; rows cover pos = pos_t-1 .. -(pos_t-1) so any T <=
+  // pos_t is a contiguous sub-range starting at row pos_t - T.
+  void ensure_pos(int t) {
+    if (t <= pos_t) return;
+    const int tt = std::max(t, 256);
+    const int rows = 2 * tt - 1;
+    std::vector<float> inv(HIDDEN / 2);
+    for (int i = 0; i < HIDDEN / 2; ++i)
+      inv[i] = 1.0f / std::pow(10000.0f, (2.0f * (float)i) / (float)HIDDEN);
+    std::vector<uint16_t> tab((size_t)(rows + 128) * HIDDEN, 0);
+    const int nth = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::vector<std::thread> th;
+    for (int w = 0; w < nth; ++w)
+      th.emplace_back([&, w] {
+        for (int pi = w; pi < rows; pi += nth) {
+          const float posv = (float)((rows - 1) / 2 - pi);
+          uint16_t* row = &tab[(size_t)pi * HIDDEN];
+          for (int i = 0; i < HIDDEN / 2; ++i) {
+            const float f = posv * inv[i];
+            row[2 * i] = f32_to_f16_bits(std::sin(f));
+            row[2 * i + 1] = f32_to_f16_bits(std::cos(f));
+          }
+        }
+      });
+    for (auto& x : th) x.join();
+    ensure(pos, tab.size() * 2);
+    BARK_HIP_CHECK(hipMemcpy(pos.p, tab.data(), tab.size() * 2, hipMemcpyHostToDevice));
+    pos_t = tt;
+  }
+
+  // ------------------------------------------------------------- forward --
+  struct Plan {
+    std::vector<SeqPlan> seqs;
+    int mp = 0;  // packed rows (multiple of 64)
+    int tc = 0;  // longest sequence: relK covers |q-k| < tc
+  };
+
+  static Plan make_plan(const int32_t* frames, const int32_t* valid, const int32_t* tlen,
+                        int batch) {
+    Plan pl;
+    int row = 0;
+    for (int i = 0; i < batch; ++i) {
+      SeqPlan s;
+      if (frames) {
+        BARK_REQUIRE(frames[i] >= 1, "n_frames must be >= 1");
+        s.frames = frames[i];
+        s.valid = valid ? valid[i] : frames[i];
+        s.t = conv_len(conv_len(conv_len(s.frames)));
+      } else {
+        s.t = tlen[i];
+      }
+      BARK_REQUIRE(s.t >= 1, "sequence length must be >= 1");
+      s.start = row;
+      row += round_up(s.t, 64);
+      pl.tc = std::max(pl.tc, s.t);
+      pl.seqs.push_back(s);
+    }
+    pl.mp = row;
+    return pl;
+  }
+
+  void ensure_workspace(const Plan& pl) {
+    const size_t mp = pl.mp;
+    const size_t pp = round_up(2 * pl.tc - 1, 64);
+    ensure(sub16, mp * 4096 * 2);
+    ensure(xn, mp * HIDDEN * 2);
+    ensure(hid, mp * FFN * 2);
+    ensure(qu, HEADS * mp * HDIM * 2);
+    ensure(qv, HEADS * mp * HDIM * 2);
+    ensure(kh, HEADS * mp * HDIM * 2);
+    ensure(vt, HEADS * mp * HDIM * 2);
+    ensure(rk, HEADS * pp * HDIM * 2);
+    ensure(ao, mp * HIDDEN * 2);
+    ensure(h, mp * HIDDEN * 4);
+    ensure(h2, mp * HIDDEN * 4);
+    ensure(glu, mp * HIDDEN * 4);
+    ensure(pooler, mp * PROJ * 4);
+    ensure(bounds, mp * sizeof(int2));
+    ensure(tiles, (mp / 64 + pl.seqs.size()) * sizeof(int4));
+    ensure_pos(pl.tc);
+  }
+
+  // Row bounds for the depthwise conv and query tiles for attention.
+  void upload_tables(const Plan& pl, hipStream_t st) {
+    std::vector<int2> b(pl.mp);
+    for (int r = 0; r < pl.mp; ++r) b[r] = make_int2(r, r + 1);
+    std::vector<int4> tl;
+    for (const auto& s : pl.seqs) {
+      for (int r = s.start; r < s.start + s.t; ++r) b[r] = make_int2(s.start, s.start + s.t);
+      for (int q0 = 0; q0 < s.t; q0 += 128) tl.push_back(make_int4(s.start, s.t, q0, 0));
+    }
+    BARK_HIP_CHECK(hipMemcpyAsync(bounds.p, b.data(), b.size() * sizeof(int2),
+                                  hipMemcpyHostToDevice, st));
+    BARK_HIP_CHECK(hipMemcpyAsync(tiles.p, tl.data(), tl.size() * sizeof(int4),
+                                  hipMemcpyHostToDevice, st));
+    ntiles = (int)tl.size();
+    BARK_HIP_CHECK(hipStreamSynchronize(st));  // host vectors go out of scope
+  }
+  int ntiles = 0;
+
+  // conv front end of one utterance into rows [s.start, s.start+s.t) of sub16.
+  void front_end(const float* d_mel, const SeqPlan& s, hipStream_t st) {
+    BARK_REQUIRE(has_front_end, "the conv subsampling weights were not loaded");
+    const int f1 = conv_len(s.frames), t2 = conv_len(f1), t3 = conv_len(t2);
+    int vlen = conv_len(std::max(s.valid, 1));
+    sub_conv1(d_mel, s.frames, l0w, l0b, y1.as<half>(), std::min(vlen, f1), st);
+    vlen = conv_len(vlen);
+    sub_dwconv(y1.as<half>(), f1, 64, l2w, l2b, y2.as<half>(), std::min(vlen, t2), st);
+    EpiArgs e1;
+    e1.out_f16 = y3.as<half>();
+    e1.ldo = SUB_CH;
+    e1.bias = l3b;
+    gemm(y2.as<half>(), SUB_CH, t2 * 32, sub_pw1, Epi::BiasReluF16, e1, st);
+    vlen = conv_len(vlen);
+    sub_dwconv(y3.as<half>(), t2, 32, l5w, l5b, y4.as<half>(), std::min(vlen, t3), st);
+    EpiArgs e2;
+    e2.out_f16 = sub16.as<half>() + (size_t)s.start * 4096;
+    e2.ldo = 4096;
+    e2.bias = l6b;
+    gemm(y4.as<half>(), SUB_CH, t3 * 16, sub_pw2, Epi::FlattenReluF16, e2, st);
+  }
+
+  void ensure_front_end(const Plan& pl) {
+    size_t n1 = 0, n2 = 0, n4 = 0;
+    for (const auto& s : pl.seqs) {
+      const int f1 = conv_len(s.frames), t2 = conv_len(f1), t3 = conv_len(t2);
+      n1 = std::max(n1, (size_t)f1 * 64 * SUB_CH);
+      n2 = std::max(n2, (size_t)t2 * 32 * SUB_CH);
+      n4 = std::max(n4, (size_t)t3 * 16 * SUB_CH);
+    }
+    ensure(y1, n1 * 2);
+    ensure(y2, n2 * 2);
+    ensure(y3, n2 * 2);
+    ensure(y4, n4 * 2);
+  }
+
+  // The 24 blocks + projector over the packed rows in sub16 (pooler rows out).
+  void encoder_blocks(const Plan& pl, int dump_layer, hipStream_t st) {
+    const int mp = pl.mp, tc = pl.tc, prows = 2 * tc - 1;
+    const int pp = round_up(prows, 64);
+    float* hc = h.as<float>();
+    float* ha = h2.as<float>();
+    half* xnp = xn.as<half>();
+
+    EpiArgs es;  // sub linear + bias -> h
+    es.out_f32 = hc;
+    es.ldo = HIDDEN;
+    es.bias = sub_b;
+    gemm(sub16.as<half>(), 4096, mp, sub_w, Epi::StoreF32, es, st);
+
+    const half* pos_rows = pos.as<half>() + (size_t)(pos_t - tc) * HIDDEN;
+    for (int l = 0; l < n_layers; ++l) {
+      const DevLayer& L = layers[l];
+      if (l == 0) layer_norm(hc, L.ln_w[0], L.ln_b[0], xnp, nullptr, mp, st);
+      // ---- FF1: h += 0.5 * W2 silu(W1 LN(h))
+      EpiArgs e;
+      e.out_f16 = hid.as<half>();
+      e.ldo = FFN;
+      gemm(xnp, HIDDEN, mp, L.ff1a, Epi::Silu, e, st);
+      e = EpiArgs();
+      e.out_f32 = hc;
+      e.ldo = HIDDEN;
+      e.scale = 0.5f;
+      gemm(hid.as<half>(), FFN, mp, L.ff1b, Epi::Resid, e, st);
+      // ---- attention
+      layer_norm(hc, L.ln_w[1], L.ln_b[1], xnp, nullptr, mp, st);
+      e = EpiArgs();
+      e.qu = qu.as<half>();
+      e.qv = qv.as<half>();
+      e.kh = kh.as<half>();
+      e.vt = vt.as<half>();
+      e.bu = L.bu;
+      e.bv = L.bv;
+      e.mp = mp;
+      gemm(xnp, HIDDEN, mp, L.qkv, Epi::Qkv, e, st);
+      e = EpiArgs();
+      e.rk = rk.as<half>();
+      e.pp = pp;
+      gemm(pos_rows, HIDDEN, prows, L.relk, Epi::RelK, e, st);
+      AttnArgs aa{qu.as<half>(), qv.as<half>(), kh.as<half>(), vt.as<half>(), rk.as<half>(),
+                  ao.as<half>(), mp, pp, tc, tiles.as<int4>(), ntiles};
+      rel_attention(aa, st);
+      e = EpiArgs();
+      e.out_f32 = hc;
+      e.ldo = HIDDEN;
+      e.scale = 1.0f;
+      gemm(ao.as<half>(), HIDDEN, mp, L.o, Epi::Resid, e, st);
+      // ---- conv module
+      layer_norm(hc, L.ln_w[2], L.ln_b[2], xnp, nullptr, mp, st);
+      e = EpiArgs();
+      e.out_f32 = glu.as<float>();
+      e.ldo = HIDDEN;
+      gemm(xnp, HIDDEN, mp, L.pw1, Epi::Glu, e, st);
+      dwconv_bn_silu(glu.as<float>(), L.dw, L.bn_a, L.bn_b, bounds.as<int2>(), xnp, mp, st);
+      e = EpiArgs();
+      e.out_f32 = hc;
+      e.ldo = HIDDEN;
+      e.scale = 1.0f;
+      gemm(xnp, HIDDEN, mp, L.pw2, Epi::Resid, e, st);
+      // ---- FF2
+      layer_norm(hc, L.ln_w[3], L.ln_b[3], xnp, nullptr, mp, st);
+      e = EpiArgs();
+      e.out_f16 = hid.as<half>();
+      e.ldo = FFN;
+      gemm(xnp, HIDDEN, mp, L.ff2a, Epi::Silu, e, st);
+      e = EpiArgs();
+      e.out_f32 = hc;
+      e.ldo = HIDDEN;
+      e.scale = 0.5f;
+      gemm(hid.as<half>(), FFN, mp, L.ff2b, Epi::Resid, e, st);
+      if (l == dump_layer) {
+        ensure(dump, (size_t)mp * HIDDEN * 4);
+        copy_rows_f32(hc, HIDDEN, dump.as<float>(), HIDDEN, mp, HIDDEN, st);
+      }
+      // ---- norm_out (fused with the next block's first LayerNorm)
+      if (l + 1 < n_layers) {
+        const DevLayer& N = layers[l + 1];
+        layer_norm2(hc, L.ln_w[4], L.ln_b[4], ha, N.ln_w[0], N.ln_b[0], xnp, mp, st);
+      } else {
+        layer_norm(hc, L.ln_w[4], L.ln_b[4], xnp, ha, mp, st);
+      }
+      std::swap(hc, ha);
+    }
+    EpiArgs ep;
+    ep.out_f32 = pooler.as<float>();
+    ep.ldo = PROJ;
+    ep.bias = proj_b;
+    gemm(xnp, HIDDEN, mp, proj_w, Epi::StoreF32, ep, st);
+  }
+
+  // Shared body of the mel-input entry points; pooler rows of sequence i are
+  // written to out + (sum of earlier t) * 640 with `kind` host or device.
+  void encode_mel_batch(const float* mel_in, bool mel_on_device, const int32_t* frames,
+                        const int32_t* valid, int batch, int32_t* t_out, float* out,
+                        bool out_on_device, size_t cap, hipStream_t st) {
+    BARK_REQUIRE(finalized, "encode before finalize");
+    BARK_REQUIRE(batch >= 1 && frames, "batch must be >= 1");
+    Plan pl = make_plan(frames, valid, nullptr, batch);
+    size_t need_out = 0, total_frames = 0;
+    for (const auto& s : pl.seqs) {
+      need_out += (size_t)s.t * PROJ;
+      total_frames += (size_t)s.frames;
+    }
+    BARK_REQUIRE(cap >= need_out, "pooler capacity too small");
+    ensure_workspace(pl);
+    ensure_front_end(pl);
+    const float* dmel = mel_in;
+    if (!mel_on_device) {
+      ensure(mel, total_frames * MEL * 4);
+      BARK_HIP_CHECK(hipMemcpyAsync(mel.p, mel_in, total_frames * MEL * 4,
+                                    hipMemcpyHostToDevice, st));
+      dmel = mel.as<float>();
+    }
+    upload_tables(pl, st);
+    BARK_HIP_CHECK(hipMemsetAsync(sub16.p, 0, (size_t)pl.mp * 4096 * 2, st));
+    size_t foff = 0;
+    for (const auto& s : pl.seqs) {
+      front_end(dmel + foff * MEL, s, st);
+      foff += s.frames;
+    }
+    encoder_blocks(pl, -1, st);
+    size_t orow = 0;
+    for (size_t i = 0; i < pl.seqs.size(); ++i) {
+      const auto& s = pl.seqs[i];
+      if (t_out) t_out[i] = s.t;
+      const float* src = pooler.as<float>() + (size_t)s.start * PROJ;
+      BARK_HIP_CHECK(hipMemcpyAsync(out + orow * PROJ, src, (size_t)s.t * PROJ * 4,
+                                    out_on_device ? hipMemcpyDeviceToDevice
+                                                  : hipMemcpyDeviceToHost,
+                                    st));
+      orow += s.t;
+    }
+    if (!out_on_device) BARK_HIP_CHECK(hipStreamSynchronize(st));
+  }
+
+  void encode_sub(const float* sub_rows, int t, int dump_layer, float* out_pooler,
+                  float* out_block) {
+    BARK_REQUIRE(finalized, "encode before finalize");
+    BARK_REQUIRE(t >= 1, "t must be >= 1");
+    BARK_REQUIRE(dump_layer < n_layers, "dump_layer out of range");
+    const int32_t tl = t;
+    Plan pl = make_plan(nullptr, nullptr, &tl, 1);
+    ensure_workspace(pl);
+    ensure(subf32, (size_t)t * 4096 * 4);
+    hipStream_t st = stream;
+    BARK_HIP_CHECK(hipMemcpyAsync(subf32.p, sub_rows, (size_t)t * 4096 * 4,
+                                  hipMemcpyHostToDevice, st));
+    upload_tables(pl, st);
+    BARK_HIP_CHECK(hipMemsetAsync(sub16.p, 0, (size_t)pl.mp * 4096 * 2, st));
+    f32_to_f16_rows(subf32.as<float>(), t, 4096, sub16.as<half>(), 4096, st);
+    encoder_blocks(pl, dump_layer, st);
+    if (out_pooler)
+      BARK_HIP_CHECK(hipMemcpyAsync(out_pooler, pooler.p, (size_t)t * PROJ * 4,
+                                    hipMemcpyDeviceToHost, st));
+    if (out_block && dump_layer >= 0)
+      BARK_HIP_CHECK(hipMemcpyAsync(out_block, dump.p, (size_t)t * HIDDEN * 4,
+                                    hipMemcpyDeviceToHost, st));
+    BARK_HIP_CHECK(hipStreamSynchronize(st));
+  }
+};
+
+// -------------------------------------------------------------------- C ABI --
+namespace {
+
+template <class F>
+int guarded(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return BARK_HIP_OK;
+  } catch (const Error& e) {
+    g_last_error = e.msg;
+    if (e.msg.find("hip") != std::string::npos) return BARK_HIP_EDEVICE;
+    if (e.msg.find("before finalize") != std::string::npos ||
+        e.msg.find("twice") != std::string::npos)
+      return BARK_HIP_ESTATE;
+    return BARK_HIP_EINVAL;
+  } catch (const std::exception& e) {
+    g_last_error = std::string("internal error: ") + e.what();
+    return BARK_HIP_EINTERNAL;
+  } catch (...) {
+    g_last_error = "internal error";
+    return BARK_HIP_EINTERNAL;
+  }
+}
+
+HostTensor& stage(BarkHip* h, const char* name) {
+  BARK_REQUIRE(h && name, "null handle or name");
+  BARK_REQUIRE(!h->finalized, "tensors cannot be set after finalize");
+  return h->staged[name];
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* bark_hip_last_error(void) { return g_last_error.c_str(); }
+
+int bark_hip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+int bark_hip_create(int device, int n_layers, BarkHip** out) {
+  return guarded([&] {
+    BARK_REQUIRE(out, "null output pointer");
+    *out = nullptr;
+    BARK_REQUIRE(n_layers >= 1 && n_layers <= 24, "n_layers must be in 1..24");
+    int n = 0;
+    BARK_HIP_CHECK(hipGetDeviceCount(&n));
+    BARK_REQUIRE(device >= 0 && device < n, "no such HIP device");
+    BARK_HIP_CHECK(hipSetDevice(device));
+    auto* h = new BarkHip();
+    h->device = device;
+    h->n_layers = n_layers;
+    hipError_t e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      delete h;
+      throw Error{std::string("hipStreamCreate: ") + hipGetErrorString(e)};
+    }
+    *out = h;
+  });
+}
+
+void bark_hip_destroy(BarkHip* h) {
+  if (!h) return;
+  (void)hipSetDevice(h->device);
+  delete h;
+}
+
+int bark_hip_set_f32(BarkHip* h, const char* name, const float* v, const int64_t* shape,
+                     int ndim) {
+  return guarded([&] {
+    BARK_REQUIRE(v && shape && ndim >= 1 && ndim <= 8, "bad f32 tensor arguments");
+    std::lock_guard<std::mutex> lk(h->mu);
+    HostTensor& t = stage(h, name);
+    t = HostTensor();
+    t.kind = HostTensor::F32;
+    t.shape.assign(shape, shape + ndim);
+    const int64_t n = t.numel();
+    BARK_REQUIRE(n > 0, "empty tensor");
+    t.f32.assign(v, v + n);
+  });
+}
+
+int bark_hip_set_f16(BarkHip* h, const char* name, const uint16_t* v, int64_t rows,
+                     int64_t cols) {
+  return guarded([&] {
+    BARK_REQUIRE(v && rows > 0 && cols > 0, "bad f16 tensor arguments");
+    std::lock_guard<std::mutex> lk(h->mu);
+    HostTensor& t = stage(h, name);
+    t = HostTensor();
+    t.kind = HostTensor::F16;
+    t.shape = {rows, cols};
+    t.rows = rows;
+    t.cols = cols;
+    t.f16.assign(v, v + rows * cols);
+  });
+}
+
+int bark_hip_set_lowbit(BarkHip* h, const char* name, const uint32_t* codes,
+                        const uint16_t* levels, uint32_t k_lev, int64_t rows, int64_t cols) {
+  return guarded([&] {
+    BARK_REQUIRE(codes && levels && rows > 0 && cols > 0, "bad low-bit tensor arguments");
+    BARK_REQUIRE(k_lev >= 1 && k_lev <= 3, "unsupported level count (1..3)");
+    BARK_REQUIRE(cols % 8 == 0, "low-bit columns must be a multiple of 8");
+    std::lock_guard<std::mutex> lk(h->mu);
+    HostTensor& t = stage(h, name);
+    t = HostTensor();
+    t.kind = HostTensor::LUT4;
+    t.shape = {rows, cols};
+    t.rows = rows;
+    t.cols = cols;
+    // u32 words with nibble col&7 of word col>>3 are, byte for byte on a
+    // little-endian host, two codes per byte with the low nibble first.
+    t.codes.resize((size_t)rows * cols / 2);
+    std::memcpy(t.codes.data(), codes, t.codes.size());
+    t.lut.resize((size_t)rows * 16);
+    for (int64_t r = 0; r < rows; ++r)
+      for (uint32_t c = 0; c < 16; ++c)
+        t.lut[r * 16 + c] = f32_to_f16_bits(expand_level(c, k_lev, levels + r * 4));
+  });
+}
+
+int bark_hip_set_lut4(BarkHip* h, const char* name, const uint8_t* codes, const uint16_t* lut16,
+                      int64_t rows, int64_t cols) {
+  return guarded([&] {
+    BARK_REQUIRE(codes && lut16 && rows > 0 && cols > 0, "bad 4-bit tensor arguments");
+    BARK_REQUIRE(cols % 2 == 0, "4-bit columns must be even");
+    std::lock_guard<std::mutex> lk(h->mu);
+    HostTensor& t = stage(h, name);
+    t = HostTensor();
+    t.kind = HostTensor::LUT4;
+    t.shape = {rows, cols};
+    t.rows = rows;
+    t.cols = cols;
+    t.codes.assign(codes, codes + rows * cols / 2);
+    t.lut.assign(lut16, lut16 + rows * 16);
+  });
+}
+
+int bark_hip_finalize(BarkHip* h) {
+  return guarded([&] {
+    BARK_REQUIRE(h, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    h->finalize();
+  });
+}
+
+int bark_hip_encode_sub(BarkHip* h, const float* sub_rows, int32_t t, int32_t dump_layer,
+                        float* pooler, float* block) {
+  return guarded([&] {
+    BARK_REQUIRE(h && sub_rows, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    h->encode_sub(sub_rows, t, dump_layer, pooler, block);
+  });
+}
+
+int bark_hip_encode_mel(BarkHip* h, const float* mel, int32_t n_frames, int32_t n_valid,
+                        int32_t* t_out, float* pooler, size_t pooler_cap) {
+  return guarded([&] {
+    BARK_REQUIRE(h && mel && pooler, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    h->encode_mel_batch(mel, false, &n_frames, &n_valid, 1, t_out, pooler, false, pooler_cap,
+                        h->stream);
+  });
+}
+
+int bark_hip_encode_mel_batch(BarkHip* h, const float* mel, const int32_t* n_frames,
+                              const int32_t* n_valid, int32_t batch, int32_t* t_out,
+                              float* pooler, size_t pooler_cap) {
+  return guarded([&] {
+    BARK_REQUIRE(h && mel && pooler, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    h->encode_mel_batch(mel, false, n_frames, n_valid, batch, t_out, pooler, false, pooler_cap,
+                        h->stream);
+  });
+}
+
+int bark_hip_encode_mel_batch_device(BarkHip* h, const float* d_mel, const int32_t* n_frames,
+                                     const int32_t* n_valid, int32_t batch, int32_t* t_out,
+                                     float* d_pooler, size_t pooler_cap, void* stream) {
+  return guarded([&] {
+    BARK_REQUIRE(h && d_mel && d_pooler, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    hipStream_t st = stream ? static_cast<hipStream_t>(stream) : h->stream;
+    h->encode_mel_batch(d_mel, true, n_frames, n_valid, batch, t_out, d_pooler, true,
+                        pooler_cap, st);
+  });
+}
+
+int bark_hip_lowbit_linear(const void* A, int32_t a_dtype, const uint8_t* codes,
+                           const uint16_t* lut16, void* C, int32_t c_dtype, int32_t T,
+                           int32_t K, int32_t N, void* stream) {
+  return guarded([&] {
+    BARK_REQUIRE(A && codes && lut16 && C, "null device pointer");
+    BARK_REQUIRE(a_dtype == 0 || a_dtype == 1, "a_dtype must be 0 (f16) or 1 (bf16)");
+    BARK_REQUIRE(c_dtype >= 0 && c_dtype <= 2, "c_dtype must be 0, 1 or 2");
+    BARK_REQUIRE(T >= 1, "T must be >= 1");
+    GemmWeight w;
+    w.codes = codes;
+    w.lut = reinterpret_cast<const half*>(lut16);
+    w.n = N;
+    w.k = K;
+    EpiArgs e;
+    e.ldo = N;
+    Epi epi = Epi::StoreF32;
+    if (c_dtype == 0) {
+      e.out_f32 = static_cast<float*>(C);
+    } else {
+      e.out_f16 = static_cast<half*>(C);
+      epi = c_dtype == 1 ? Epi::StoreF16 : Epi::StoreBF16;
+    }
+    gemm(static_cast<const half*>(A), K, T, w, epi, e, static_cast<hipStream_t>(stream),
+         a_dtype == 1);
+  });
+}
+
+}  // extern "C"

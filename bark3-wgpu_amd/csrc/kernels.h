@@ -1,0 +1,92 @@
+// Host-side launchers for the gfx950 kernels (implemented in gemm.hip,
+// attention.hip, ops.hip). All take device pointers and a stream, validate the
+// shapes the kernels assume, and throw bark::Error on a mismatch.
+#pragma once
+
+#include "common.h"
+
+namespace bark {
+
+// ---------------------------------------------------------------- GEMM --
+// C[m, n] = sum_k A[m, k] * W[n, k]  (A f16 row-major, W f16 row-major or
+// 4-bit codes + per-row 16-entry f16 table), f32 accumulation on MFMA, and an
+// epilogue that consumes the f32 tile.
+enum class Epi : int {
+  StoreF32 = 0,      // out_f32[r][c] = v (+ bias[c])
+  StoreF16 = 1,      // out_f16[r][c] = f16(v (+ bias[c]))
+  Silu = 2,          // out_f16[r][c] = f16(silu(v))
+  Resid = 3,         // out_f32[r][c] += scale * v
+  Glu = 4,           // out_f32[r][c/2 pair] = a * sigmoid(b) (rows of W interleaved)
+  Qkv = 5,           // head packing of q+bias_u, q+bias_v, k, v^T (f16)
+  RelK = 6,          // rk[h][r][d] = f16(v)
+  BiasReluF16 = 7,   // out_f16[r][c] = f16(max(v + bias[c], 0))
+  FlattenReluF16 = 8, // pixel r = (t, m): out_f16[t][c*16+m] = f16(max(v+bias[c],0))
+  StoreBF16 = 9       // out (bf16 bits in out_f16)[r][c] = bf16(v (+ bias[c]))
+};
+
+struct GemmWeight {
+  // exactly one of (w16) or (codes, lut) is set
+  const half* w16 = nullptr;     // (n, k) f16
+  const uint8_t* codes = nullptr;  // (n, k/2) bytes, low nibble = even k
+  const half* lut = nullptr;     // (n, 16) f16
+  int n = 0, k = 0;
+  bool lut4() const { return codes != nullptr; }
+};
+
+struct EpiArgs {
+  float* out_f32 = nullptr;
+  half* out_f16 = nullptr;
+  int ldo = 0;
+  const float* bias = nullptr;
+  float scale = 1.0f;
+  // Qkv
+  half *qu = nullptr, *qv = nullptr, *kh = nullptr, *vt = nullptr;
+  const float *bu = nullptr, *bv = nullptr;
+  int mp = 0;  // rows of the head-major buffers
+  // RelK
+  half* rk = nullptr;
+  int pp = 0;  // rows of rk per head
+};
+
+// Rows >= M of A read as zero and are not stored. a_bf16: A holds bf16 bits
+// (converted to f16 while staging; exact for |a| in the f16 normal range).
+void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const EpiArgs& ea,
+          hipStream_t stream, bool a_bf16 = false);
+
+// ----------------------------------------------------------- attention --
+// One entry per 128-query tile: {row of the sequence's first frame, sequence
+// length, first query of the tile (local), 0}.
+struct AttnArgs {
+  const half *qu, *qv, *kh, *vt, *rk;
+  half* out;       // (mp, 1024) heads-flat
+  int mp;          // rows of qu/qv/kh and columns of vt
+  int pp;          // rows of rk per head
+  int tc;          // rk row j <-> relative position r = tc - 1 - j
+  const int4* tiles;
+  int ntiles;
+};
+void rel_attention(const AttnArgs& a, hipStream_t stream);
+
+// ----------------------------------------------------------------- ops --
+// LayerNorm over 1024 columns. y16 and/or y32 may be null.
+void layer_norm(const float* x, const float* w, const float* b, half* y16, float* y32,
+                int rows, hipStream_t stream);
+// y32 = LN_a(x) (written), y16 = f16(LN_b(y32)).
+void layer_norm2(const float* x, const float* wa, const float* ba, float* y32,
+                 const float* wb, const float* bb, half* y16, int rows, hipStream_t stream);
+// out = f16(silu(BN(dwconv9(g)))) with per-row [start, end) frame bounds.
+void dwconv_bn_silu(const float* g, const float* dw, const float* bn_a, const float* bn_b,
+                    const int2* bounds, half* out, int rows, hipStream_t stream);
+void f32_to_f16(const float* x, half* y, size_t n, hipStream_t stream);
+void f32_to_f16_rows(const float* x, int rows, int cols, half* y, int ldy,
+                     hipStream_t stream);
+void copy_rows_f32(const float* x, int ldx, float* y, int ldy, int rows, int cols,
+                   hipStream_t stream);
+// Front end. conv1: mel (frames, 128) f32 -> (f1, 64, 256) f16, ReLU, rows >= vlen zeroed.
+void sub_conv1(const float* mel, int frames, const float* w, const float* b, half* out,
+               int vlen, hipStream_t stream);
+// depthwise 3x3 stride 2 on (t_in, m_in, 256) -> (t_out, m_out, 256), rows >= vlen zeroed.
+void sub_dwconv(const half* in, int t_in, int m_in, const float* w, const float* b,
+                half* out, int vlen, hipStream_t stream);
+
+}  // namespace bark

@@ -1,0 +1,281 @@
+// Row-wise and elementwise kernels of the encoder block and the conv front end.
+// All are HBM-bound: each reads its input once and writes its output once.
+#include "kernels.h"
+
+namespace bark {
+namespace {
+
+// ---------------------------------------------------------------- LayerNorm --
+// One wave per 1024-wide row; lane l holds columns 4l + 256i (i < 4) so every
+// load is a coalesced float4. mean = E[x], var = E[x^2] - mean^2 and
+// y = (x - mean) * (1/sqrt(var + 1e-5)) * w + b, the reference formula
+// (src/encoder/shader_sources.rs:185-228, src/cpu/ops.rs:15-56).
+__device__ inline void ln_row(float (&x)[16], const float* w, const float* b, int lane) {
+  float s = 0.0f, q = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    s += x[i];
+    q += x[i] * x[i];
+  }
+  s = wave_sum(s);
+  q = wave_sum(q);
+  const float mean = s * (1.0f / 1024.0f);
+  const float var = q * (1.0f / 1024.0f) - mean * mean;
+  const float inv = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = 4 * lane + 256 * i;
+    const floatx4 wv = *reinterpret_cast<const floatx4*>(w + c);
+    const floatx4 bv = *reinterpret_cast<const floatx4*>(b + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[4 * i + e] = (x[4 * i + e] - mean) * inv * wv[e] + bv[e];
+  }
+}
+
+__device__ inline void load_row(const float* x, float (&v)[16], int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const floatx4 t = *reinterpret_cast<const floatx4*>(x + 4 * lane + 256 * i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * i + e] = t[e];
+  }
+}
+
+__device__ inline void store_row32(float* y, const float (&v)[16], int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const floatx4 t = {v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]};
+    *reinterpret_cast<floatx4*>(y + 4 * lane + 256 * i) = t;
+  }
+}
+
+__device__ inline void store_row16(half* y, const float (&v)[16], int lane) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const half4 t = {(half)v[4 * i], (half)v[4 * i + 1], (half)v[4 * i + 2], (half)v[4 * i + 3]};
+    *reinterpret_cast<half4*>(y + 4 * lane + 256 * i) = t;
+  }
+}
+
+__global__ void __launch_bounds__(256) ln_kernel(const float* x, const float* w, const float* b,
+                                                 half* y16, float* y32, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  float v[16];
+  load_row(x + (size_t)r * HIDDEN, v, lane);
+  ln_row(v, w, b, lane);
+  if (y32) store_row32(y32 + (size_t)r * HIDDEN, v, lane);
+  if (y16) store_row16(y16 + (size_t)r * HIDDEN, v, lane);
+}
+
+// Block-final norm_out of layer l fused with norm_feed_forward1 of layer l+1.
+__global__ void __launch_bounds__(256) ln2_kernel(const float* x, const float* wa,
+                                                  const float* ba, float* y32, const float* wb,
+                                                  const float* bb, half* y16, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  float v[16];
+  load_row(x + (size_t)r * HIDDEN, v, lane);
+  ln_row(v, wa, ba, lane);
+  store_row32(y32 + (size_t)r * HIDDEN, v, lane);
+  ln_row(v, wb, bb, lane);
+  store_row16(y16 + (size_t)r * HIDDEN, v, lane);
+}
+
+// ------------------------------------------------- depthwise conv + BN + SiLU --
+// y[t,c] = sum_{i<9} x[t+i-4, c] * w[c,i] over frames inside the row's
+// sequence [start, end) (zero padding at the sequence edge, the length mask
+// of src/encoder/shader_sources.rs:344-376 / src/cpu/ops.rs:195-233), then
+// z = silu(y * a_c + b_c) with the folded BatchNorm. Each thread owns one
+// channel and 32 consecutive rows; the 40-row window is read once.
+constexpr int DW_ROWS = 32;
+
+__global__ void __launch_bounds__(256) dwconv_kernel(const float* g, const float* dw,
+                                                     const float* bn_a, const float* bn_b,
+                                                     const int2* bounds, half* out, int rows) {
+  const int c = blockIdx.y * 256 + threadIdx.x;
+  const int r0 = blockIdx.x * DW_ROWS;
+  float w[9];
+#pragma unroll
+  for (int i = 0; i < 9; ++i) w[i] = dw[c * 9 + i];
+  const float a = bn_a[c], b = bn_b[c];
+  float win[DW_ROWS + 8];
+#pragma unroll
+  for (int i = 0; i < DW_ROWS + 8; ++i) {
+    const int r = r0 - 4 + i;
+    win[i] = (r >= 0 && r < rows) ? g[(size_t)r * HIDDEN + c] : 0.0f;
+  }
+#pragma unroll
+  for (int t = 0; t < DW_ROWS; ++t) {
+    const int r = r0 + t;
+    if (r >= rows) break;
+    const int2 be = bounds[r];
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 9; ++i) {
+      const int rr = r + i - 4;
+      if (rr >= be.x && rr < be.y) acc = __fadd_rn(acc, __fmul_rn(win[t + i], w[i]));
+    }
+    const float y = __fadd_rn(__fmul_rn(acc, a), b);
+    out[(size_t)r * HIDDEN + c] = (half)silu(y);
+  }
+}
+
+// ---------------------------------------------------------------- converts --
+__global__ void f32_to_f16_kernel(const float* x, half* y, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (half)x[i];
+}
+
+__global__ void f32_to_f16_rows_kernel(const float* x, int cols, half* y, int ldy, int rows) {
+  const int r = blockIdx.y;
+  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += gridDim.x * blockDim.x)
+    y[(size_t)r * ldy + c] = (half)x[(size_t)r * cols + c];
+}
+
+__global__ void copy_rows_kernel(const float* x, int ldx, float* y, int ldy, int cols) {
+  const int r = blockIdx.y;
+  for (int c = blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += gridDim.x * blockDim.x)
+    y[(size_t)r * ldy + c] = x[(size_t)r * ldx + c];
+}
+
+// -------------------------------------------------------------- front end --
+// conv 1->256, 3x3, stride 2, pad 1, then ReLU (src/sub.rs:116-168). Output
+// layout is pixel-major with channels contiguous: out[(i*64 + j)*256 + c].
+// The sum is b + w0*x0 + ... + w8*x8 in tap order with separate multiply and
+// add roundings, as the reference AXPY does; rows i >= vlen are zeroed
+// (mask_time, src/sub.rs:288-300).
+constexpr int C1_PIX = 8;  // output pixels (along mel) per workgroup
+
+__global__ void __launch_bounds__(256) conv1_kernel(const float* mel, int frames,
+                                                    const float* w, const float* b, half* out,
+                                                    int vlen) {
+  __shared__ float patch[3][2 * C1_PIX + 1];
+  const int i = blockIdx.y;               // output frame
+  const int j0 = blockIdx.x * C1_PIX;     // first output mel bin
+  const int c = threadIdx.x;
+  if (threadIdx.x < 3 * (2 * C1_PIX + 1)) {
+    const int pr = threadIdx.x / (2 * C1_PIX + 1), pc = threadIdx.x % (2 * C1_PIX + 1);
+    const int si = 2 * i + pr - 1, sj = 2 * j0 + pc - 1;
+    patch[pr][pc] = (si >= 0 && si < frames && sj >= 0 && sj < MEL) ? mel[(size_t)si * MEL + sj] : 0.0f;
+  }
+  __syncthreads();
+  float wr[9];
+#pragma unroll
+  for (int t = 0; t < 9; ++t) wr[t] = w[c * 9 + t];
+  const float bias = b[c];
+  const bool masked = i >= vlen;
+#pragma unroll
+  for (int p = 0; p < C1_PIX; ++p) {
+    float acc = bias;
+#pragma unroll
+    for (int t = 0; t < 9; ++t)
+      acc = __fadd_rn(acc, __fmul_rn(wr[t], patch[t / 3][2 * p + t % 3]));
+    acc = acc > 0.0f ? acc : 0.0f;
+    if (masked) acc = 0.0f;
+    out[((size_t)i * 64 + j0 + p) * SUB_CH + c] = (half)acc;
+  }
+}
+
+// depthwise 3x3 stride 2 pad 1 (src/sub.rs:174-203): s = b + sum w*x over the
+// in-range taps in (ki, kj) order; rows >= vlen zeroed.
+constexpr int DW2_PIX = 4;
+
+__global__ void __launch_bounds__(256) sub_dw_kernel(const half* in, int t_in, int m_in,
+                                                     const float* w, const float* b, half* out,
+                                                     int t_out, int m_out, int vlen) {
+  const int c = threadIdx.x;
+  float wr[9];
+#pragma unroll
+  for (int t = 0; t < 9; ++t) wr[t] = w[c * 9 + t];
+  const float bias = b[c];
+  const int npix = t_out * m_out;
+  for (int p = 0; p < DW2_PIX; ++p) {
+    const int pix = blockIdx.x * DW2_PIX + p;
+    if (pix >= npix) break;
+    const int i = pix / m_out, j = pix % m_out;
+    float s = bias;
+#pragma unroll
+    for (int ki = 0; ki < 3; ++ki) {
+      const int ii = 2 * i + ki - 1;
+      if (ii < 0 || ii >= t_in) continue;
+#pragma unroll
+      for (int kj = 0; kj < 3; ++kj) {
+        const int jj = 2 * j + kj - 1;
+        if (jj < 0 || jj >= m_in) continue;
+        const float x = (float)in[((size_t)ii * m_in + jj) * SUB_CH + c];
+        s = __fadd_rn(s, __fmul_rn(wr[ki * 3 + kj], x));
+      }
+    }
+    if (i >= vlen) s = 0.0f;
+    out[(size_t)pix * SUB_CH + c] = (half)s;
+  }
+}
+
+}  // namespace
+
+void layer_norm(const float* x, const float* w, const float* b, half* y16, float* y32,
+                int rows, hipStream_t stream) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(ln_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, w, b, y16,
+                     y32, rows);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
+void layer_norm2(const float* x, const float* wa, const float* ba, float* y32, const float* wb,
+                 const float* bb, half* y16, int rows, hipStream_t stream) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(ln2_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, wa, ba,
+                     y32, wb, bb, y16, rows);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
+void dwconv_bn_silu(const float* g, const float* dw, const float* bn_a, const float* bn_b,
+                    const int2* bounds, half* out, int rows, hipStream_t stream) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(dwconv_kernel, dim3(ceil_div(rows, DW_ROWS), HIDDEN / 256), dim3(256), 0,
+                     stream, g, dw, bn_a, bn_b, bounds, out, rows);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
+void f32_to_f16(const float* x, half* y, size_t n, hipStream_t stream) {
+  if (n == 0) return;
+  hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     x, y, n);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
+void f32_to_f16_rows(const float* x, int rows, int cols, half* y, int ldy, hipStream_t stream) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(f32_to_f16_rows_kernel, dim3(ceil_div(cols, 256), rows), dim3(256), 0,
+                     stream, x, cols, y, ldy, rows);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
+void copy_rows_f32(const float* x, int ldx, float* y, int ldy, int rows, int cols,
+                   hipStream_t stream) {
+  if (rows <= 0) return;
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(ceil_div(cols, 256), rows), dim3(256), 0, stream, x,
+                     ldx, y, ldy, cols);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
+void sub_conv1(const float* mel, int frames, const float* w, const float* b, half* out,
+               int vlen, hipStream_t stream) {
+  const int f1 = (frames - 1) / 2 + 1;
+  hipLaunchKernelGGL(conv1_kernel, dim3(64 / C1_PIX, f1), dim3(256), 0, stream, mel, frames, w,
+                     b, out, vlen);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
+void sub_dwconv(const half* in, int t_in, int m_in, const float* w, const float* b, half* out,
+                int vlen, hipStream_t stream) {
+  const int t_out = (t_in - 1) / 2 + 1, m_out = (m_in - 1) / 2 + 1;
+  hipLaunchKernelGGL(sub_dw_kernel, dim3(ceil_div(t_out * m_out, DW2_PIX)), dim3(256), 0,
+                     stream, in, t_in, m_in, w, b, out, t_out, m_out, vlen);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace bark

@@ -1,0 +1,121 @@
+/*
+ * bark_hip — C ABI of the MI355X (gfx950) Conformer encoder backend.
+ *
+ * The reference (eclipse005/bark3-wgpu, Rust) drives its GPU encoder through
+ * `AsrInference::load` -> `Encoder::load_with` -> `Encoder::encode[_pre]` and
+ * its conv front end through `SubGpu::run`. These entry points are what a
+ * `Backend::Hip` arm binds over FFI in place of those calls (see
+ * INTEGRATION.md for the Rust `extern "C"` block).
+ *
+ * Conventions
+ *  - Every function returns 0 on success and a negative code on error; the
+ *    message is available from bark_hip_last_error() (thread-local), the
+ *    counterpart of the reference's `anyhow::Error`.
+ *  - Host pointers are borrowed for the duration of the call only.
+ *  - Calls on one handle are serialised by an internal mutex (the reference
+ *    shares `&AsrInference` across threads, src/inference.rs:17-18).
+ *  - No C++ exceptions cross this boundary.
+ */
+#ifndef BARK_HIP_H
+#define BARK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct BarkHip BarkHip;
+
+enum {
+  BARK_HIP_OK = 0,
+  BARK_HIP_EINVAL = -1,  /* bad argument / shape / unknown tensor name */
+  BARK_HIP_ESTATE = -2,  /* call out of order (e.g. encode before finalize) */
+  BARK_HIP_EDEVICE = -3, /* HIP runtime error, no device */
+  BARK_HIP_EINTERNAL = -4
+};
+
+/* Thread-local description of the last error on this thread. */
+const char *bark_hip_last_error(void);
+
+/* Number of visible HIP devices (0 when none): the probe behind
+ * `Backend::Auto`'s fall-back to the CPU path (src/inference.rs:219-229). */
+int bark_hip_device_count(void);
+
+/* Replaces Gpu::new_with + the start of Encoder::load_with
+ * (src/gpu.rs:448, src/encoder.rs:412). `n_layers` is 24 for the real model;
+ * fewer blocks are accepted for tests. */
+int bark_hip_create(int device, int n_layers, BarkHip **out);
+void bark_hip_destroy(BarkHip *h);
+
+/* ---- weight ingest: one call per reference tensor name -----------------
+ * Names are the reference's (src/encoder.rs:423-604, src/sub.rs:85-89), e.g.
+ * "encoder.layers.3.feed_forward1.linear1.weight". Values are the checkpoint
+ * values in the stated encoding; the library keeps its own copy. */
+
+/* f32 values (RawTensor::to_f32, src/raw.rs:23-48). Linear weights given this
+ * way are rounded to f16 (RNE) like RawTensor::to_f16_words (src/raw.rs:66-97). */
+int bark_hip_set_f32(BarkHip *h, const char *name, const float *v, const int64_t *shape,
+                     int ndim);
+/* f16 bits (rows, cols) row-major (RawTensor::to_f16_words, src/raw.rs:66-97). */
+int bark_hip_set_f16(BarkHip *h, const char *name, const uint16_t *v, int64_t rows,
+                     int64_t cols);
+/* The reference's low-bit layout (LowBitTensor, src/bark.rs:31-48;
+ * upload_lowbit, src/encoder.rs:288-317): codes rows x ceil(cols/8) u32, nibble
+ * col&7 of word col>>3; levels rows x 4 f16, k_lev in 1..3. Expanded on load
+ * to the 16-entry table lut[c] = expand(c, k_lev, levels) (src/bark.rs:597-611). */
+int bark_hip_set_lowbit(BarkHip *h, const char *name, const uint32_t *codes,
+                        const uint16_t *levels, uint32_t k_lev, int64_t rows, int64_t cols);
+/* Generic 4-bit format: codes rows x cols/2 bytes (two per byte, low nibble =
+ * even column), lut16 rows x 16 f16. Byte-identical code layout to the above. */
+int bark_hip_set_lut4(BarkHip *h, const char *name, const uint8_t *codes,
+                      const uint16_t *lut16, int64_t rows, int64_t cols);
+/* Fuses q|k|v (load_qkv, src/encoder.rs:342-402), folds BatchNorm
+ * (src/encoder.rs:546-557), interleaves pw1 rows for the GLU epilogue and
+ * uploads everything. Returns BARK_HIP_EINVAL naming a missing tensor. */
+int bark_hip_finalize(BarkHip *h);
+
+/* ---- forward ------------------------------------------------------------ */
+
+/* Encoder::encode (src/encoder.rs:1985-2001): sub_rows (t, 4096) f32 host ->
+ * pooler (t, 640) f32 host. block: if dump_layer >= 0, receives the pre-norm
+ * residual (t, 1024) of that block (src/encoder.rs:2598-2606); may be NULL. */
+int bark_hip_encode_sub(BarkHip *h, const float *sub_rows, int32_t t, int32_t dump_layer,
+                        float *pooler, float *block);
+
+/* SubGpu::run + Encoder::encode_pre (src/sub_gpu.rs:574-776,
+ * src/encoder.rs:2005-2657): mel (n_frames, 128) f32 host -> pooler. t_out
+ * receives T = conv_len^3(n_frames); pooler_cap is the capacity in floats. */
+int bark_hip_encode_mel(BarkHip *h, const float *mel, int32_t n_frames, int32_t n_valid,
+                        int32_t *t_out, float *pooler, size_t pooler_cap);
+
+/* Batched form for chunked / multi-utterance input (src/inference.rs:311-326
+ * runs the chunks one after another). mel holds the utterances back to back;
+ * each result equals that utterance's own bark_hip_encode_mel. Sequences are
+ * packed without padding between them apart from 64-row alignment; weights
+ * are streamed once per batch. pooler receives sum(t_out[i]) rows. */
+int bark_hip_encode_mel_batch(BarkHip *h, const float *mel, const int32_t *n_frames,
+                              const int32_t *n_valid, int32_t batch, int32_t *t_out,
+                              float *pooler, size_t pooler_cap);
+
+/* Device-resident form of bark_hip_encode_mel_batch: d_mel and d_pooler are
+ * device pointers, work is queued on `stream` (a hipStream_t; NULL = the
+ * handle's stream) and the call returns without synchronising. */
+int bark_hip_encode_mel_batch_device(BarkHip *h, const float *d_mel, const int32_t *n_frames,
+                                     const int32_t *n_valid, int32_t batch, int32_t *t_out,
+                                     float *d_pooler, size_t pooler_cap, void *stream);
+
+/* Isolated 4-bit level-table linear (one bm64_lb dispatch of Ctx::gemm_f32,
+ * src/encoder.rs:1039-1100, in the generic table format): device pointers
+ * A (T, K) activations, codes (N, K/2) bytes, lut16 (N, 16) f16, C (T, N).
+ * a_dtype: 0 = f16, 1 = bf16. c_dtype: 0 = f32, 1 = f16, 2 = bf16.
+ * K % 64 == 0, N % 128 == 0. Queued on `stream`, not synchronised. */
+int bark_hip_lowbit_linear(const void *A, int32_t a_dtype, const uint8_t *codes,
+                           const uint16_t *lut16, void *C, int32_t c_dtype, int32_t T,
+                           int32_t K, int32_t N, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
