@@ -139,6 +139,8 @@ _SIGS = {
             _c.c_void_p, _c.c_size_t, _c.c_void_p,
         ],
     ),
+    "bark_hip_profile": (_c.c_int, [_c.c_void_p, _c.c_int]),
+    "bark_hip_profile_report": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_size_t]),
     "bark_hip_lowbit_linear": (
         _c.c_int,
         [
@@ -309,6 +311,18 @@ class HipEncoder:
             )
         )
         return t_out
+
+    def profile(self, enable: bool = True) -> None:
+        """Per-operator HIP-event timing of the forward (BARK3_ENC_PROFILE)."""
+        _check(lib().bark_hip_profile(self._h, 1 if enable else 0))
+
+    def profile_report(self) -> dict:
+        """{label: {count, ms, flops, bytes}} since the last report."""
+        import json
+
+        buf = ctypes.create_string_buffer(1 << 16)
+        _check(lib().bark_hip_profile_report(self._h, buf, len(buf)))
+        return json.loads(buf.value.decode())
 
     def close(self) -> None:
         if getattr(self, "_h", None):

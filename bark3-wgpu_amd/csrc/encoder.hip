@@ -89,6 +89,82 @@ struct DevBuf {
   }
 };
 
+// Per-operator GPU timing, the counterpart of the reference's
+// BARK3_ENC_PROFILE timestamps (src/encoder/prof.rs:1-127): when enabled, every
+// launch is bracketed by two events on its stream; report() aggregates the
+// elapsed times per label together with the algorithmic FLOPs and bytes.
+struct Profiler {
+  struct Op {
+    std::string label;
+    double flops, bytes;
+    hipEvent_t a, b;
+  };
+  bool on = false;
+  std::vector<hipEvent_t> free_events;
+  std::vector<Op> ops;
+
+  hipEvent_t take() {
+    if (free_events.empty()) {
+      hipEvent_t e;
+      BARK_HIP_CHECK(hipEventCreate(&e));
+      return e;
+    }
+    hipEvent_t e = free_events.back();
+    free_events.pop_back();
+    return e;
+  }
+  template <class F>
+  void run(const char* label, double flops, double bytes, hipStream_t st, F&& f) {
+    if (!on) {
+      f();
+      return;
+    }
+    Op op{label, flops, bytes, take(), take()};
+    BARK_HIP_CHECK(hipEventRecord(op.a, st));
+    f();
+    BARK_HIP_CHECK(hipEventRecord(op.b, st));
+    ops.push_back(op);
+  }
+  std::string report() {
+    struct Agg {
+      int count = 0;
+      double ms = 0, flops = 0, bytes = 0;
+    };
+    std::map<std::string, Agg> agg;
+    for (auto& op : ops) {
+      BARK_HIP_CHECK(hipEventSynchronize(op.b));
+      float ms = 0;
+      BARK_HIP_CHECK(hipEventElapsedTime(&ms, op.a, op.b));
+      Agg& g = agg[op.label];
+      g.count++;
+      g.ms += ms;
+      g.flops += op.flops;
+      g.bytes += op.bytes;
+      free_events.push_back(op.a);
+      free_events.push_back(op.b);
+    }
+    ops.clear();
+    std::string out = "{";
+    bool first = true;
+    for (auto& kv : agg) {
+      char buf[256];
+      snprintf(buf, sizeof buf, "%s\"%s\":{\"count\":%d,\"ms\":%.6f,\"flops\":%.6e,\"bytes\":%.6e}",
+               first ? "" : ",", kv.first.c_str(), kv.second.count, kv.second.ms, kv.second.flops,
+               kv.second.bytes);
+      out += buf;
+      first = false;
+    }
+    return out + "}";
+  }
+  ~Profiler() {
+    for (auto& op : ops) {
+      (void)hipEventDestroy(op.a);
+      (void)hipEventDestroy(op.b);
+    }
+    for (auto e : free_events) (void)hipEventDestroy(e);
+  }
+};
+
 struct SeqPlan {
   int frames = 0, valid = 0;
   int t = 0;      // encoder frames
@@ -110,6 +186,8 @@ struct BarkHip {
   bool has_front_end = false;
 
   std::vector<void*> allocs;  // weights, freed at destroy
+  Profiler prof;
+  std::vector<int> table_key;  // plan whose row bounds / query tiles are on the device
   GemmWeight sub_w, proj_w, sub_pw1, sub_pw2;
   float *sub_b = nullptr, *proj_b = nullptr;
   float *l0w = nullptr, *l0b = nullptr, *l2w = nullptr, *l2b = nullptr, *l3b = nullptr;
@@ -135,7 +213,8 @@ struct BarkHip {
 
   void ensure(DevBuf& b, size_t bytes) {
     if (bytes <= b.cap) return;
-    BARK_HIP_CHECK(hipStreamSynchronize(stream));
+    if (&b == &bounds || &b == &tiles) table_key.clear();
+    BARK_HIP_CHECK(hipDeviceSynchronize());  // any stream may still use the old buffer
     if (b.p) BARK_HIP_CHECK(hipFree(b.p));
     b.p = nullptr;
     b.cap = 0;
@@ -414,6 +493,12 @@ struct BarkHip {
 
   // Row bounds for the depthwise conv and query tiles for attention.
   void upload_tables(const Plan& pl, hipStream_t st) {
+    std::vector<int> key{pl.mp};
+    for (const auto& s : pl.seqs) {
+      key.push_back(s.start);
+      key.push_back(s.t);
+    }
+    if (key == table_key) return;  // same packing as the previous call
     std::vector<int2> b(pl.mp);
     for (int r = 0; r < pl.mp; ++r) b[r] = make_int2(r, r + 1);
     std::vector<int4> tl;
@@ -427,29 +512,52 @@ struct BarkHip {
                                   hipMemcpyHostToDevice, st));
     ntiles = (int)tl.size();
     BARK_HIP_CHECK(hipStreamSynchronize(st));  // host vectors go out of scope
+    table_key = key;
   }
   int ntiles = 0;
+
+  // Algorithmic bytes of a linear's weight operand.
+  static double weight_bytes(const GemmWeight& w) {
+    return w.lut4() ? (double)w.n * w.k / 2 + 32.0 * w.n : 2.0 * w.n * w.k;
+  }
+
+  // One profiled GEMM: flops = 2*m_real*N*K, bytes = weights + A + output.
+  void gemm_op(const char* label, const half* A, int lda, int M, int m_real, const GemmWeight& W,
+               Epi epi, const EpiArgs& e, double out_bytes_per_row, hipStream_t st) {
+    const double flops = 2.0 * m_real * W.n * W.k;
+    const double bytes = weight_bytes(W) + 2.0 * m_real * W.k + out_bytes_per_row * m_real;
+    prof.run(label, flops, bytes, st, [&] { gemm(A, lda, M, W, epi, e, st); });
+  }
 
   // conv front end of one utterance into rows [s.start, s.start+s.t) of sub16.
   void front_end(const float* d_mel, const SeqPlan& s, hipStream_t st) {
     BARK_REQUIRE(has_front_end, "the conv subsampling weights were not loaded");
     const int f1 = conv_len(s.frames), t2 = conv_len(f1), t3 = conv_len(t2);
     int vlen = conv_len(std::max(s.valid, 1));
-    sub_conv1(d_mel, s.frames, l0w, l0b, y1.as<half>(), std::min(vlen, f1), st);
+    const double p1 = (double)f1 * 64, p2 = (double)t2 * 32, p3 = (double)t3 * 16;
+    prof.run("fe_conv1", 2.0 * 9 * 256 * p1, 4.0 * s.frames * MEL + 2.0 * 256 * p1, st, [&] {
+      sub_conv1(d_mel, s.frames, l0w, l0b, y1.as<half>(), std::min(vlen, f1), st);
+    });
     vlen = conv_len(vlen);
-    sub_dwconv(y1.as<half>(), f1, 64, l2w, l2b, y2.as<half>(), std::min(vlen, t2), st);
+    prof.run("fe_dwconv", 2.0 * 9 * 256 * p2, 2.0 * 256 * (p1 + p2), st, [&] {
+      sub_dwconv(y1.as<half>(), f1, 64, l2w, l2b, y2.as<half>(), std::min(vlen, t2), st);
+    });
     EpiArgs e1;
     e1.out_f16 = y3.as<half>();
     e1.ldo = SUB_CH;
     e1.bias = l3b;
-    gemm(y2.as<half>(), SUB_CH, t2 * 32, sub_pw1, Epi::BiasReluF16, e1, st);
+    gemm_op("fe_pointwise", y2.as<half>(), SUB_CH, t2 * 32, t2 * 32, sub_pw1, Epi::BiasReluF16, e1,
+            2.0 * SUB_CH, st);
     vlen = conv_len(vlen);
-    sub_dwconv(y3.as<half>(), t2, 32, l5w, l5b, y4.as<half>(), std::min(vlen, t3), st);
+    prof.run("fe_dwconv", 2.0 * 9 * 256 * p3, 2.0 * 256 * (p2 + p3), st, [&] {
+      sub_dwconv(y3.as<half>(), t2, 32, l5w, l5b, y4.as<half>(), std::min(vlen, t3), st);
+    });
     EpiArgs e2;
     e2.out_f16 = sub16.as<half>() + (size_t)s.start * 4096;
     e2.ldo = 4096;
     e2.bias = l6b;
-    gemm(y4.as<half>(), SUB_CH, t3 * 16, sub_pw2, Epi::FlattenReluF16, e2, st);
+    gemm_op("fe_pointwise", y4.as<half>(), SUB_CH, t3 * 16, t3 * 16, sub_pw2, Epi::FlattenReluF16, e2,
+            2.0 * SUB_CH, st);
   }
 
   void ensure_front_end(const Plan& pl) {
@@ -466,36 +574,46 @@ struct BarkHip {
     ensure(y4, n4 * 2);
   }
 
-  // The 24 blocks + projector over the packed rows in sub16 (pooler rows out).
+  // The blocks + projector over the packed rows in sub16 (pooler rows out).
   void encoder_blocks(const Plan& pl, int dump_layer, hipStream_t st) {
     const int mp = pl.mp, tc = pl.tc, prows = 2 * tc - 1;
     const int pp = round_up(prows, 64);
+    int mr = 0;  // real frames (algorithmic work excludes alignment rows)
+    double attn_flops = 0;
+    for (const auto& q : pl.seqs) {
+      mr += q.t;
+      attn_flops += 6144.0 * q.t * q.t;  // content + in-band position + AV
+    }
     float* hc = h.as<float>();
     float* ha = h2.as<float>();
     half* xnp = xn.as<half>();
+    const double ln_bytes = (double)mr * HIDDEN * (4 + 2);
 
     EpiArgs es;  // sub linear + bias -> h
     es.out_f32 = hc;
     es.ldo = HIDDEN;
     es.bias = sub_b;
-    gemm(sub16.as<half>(), 4096, mp, sub_w, Epi::StoreF32, es, st);
+    gemm_op("sub_linear", sub16.as<half>(), 4096, mp, mr, sub_w, Epi::StoreF32, es, 4.0 * HIDDEN, st);
 
     const half* pos_rows = pos.as<half>() + (size_t)(pos_t - tc) * HIDDEN;
     for (int l = 0; l < n_layers; ++l) {
       const DevLayer& L = layers[l];
-      if (l == 0) layer_norm(hc, L.ln_w[0], L.ln_b[0], xnp, nullptr, mp, st);
+      if (l == 0)
+        prof.run("layernorm", 0, ln_bytes, st,
+                 [&] { layer_norm(hc, L.ln_w[0], L.ln_b[0], xnp, nullptr, mp, st); });
       // ---- FF1: h += 0.5 * W2 silu(W1 LN(h))
       EpiArgs e;
       e.out_f16 = hid.as<half>();
       e.ldo = FFN;
-      gemm(xnp, HIDDEN, mp, L.ff1a, Epi::Silu, e, st);
+      gemm_op("ff_up_silu", xnp, HIDDEN, mp, mr, L.ff1a, Epi::Silu, e, 2.0 * FFN, st);
       e = EpiArgs();
       e.out_f32 = hc;
       e.ldo = HIDDEN;
       e.scale = 0.5f;
-      gemm(hid.as<half>(), FFN, mp, L.ff1b, Epi::Resid, e, st);
+      gemm_op("ff_down_resid", hid.as<half>(), FFN, mp, mr, L.ff1b, Epi::Resid, e, 8.0 * HIDDEN, st);
       // ---- attention
-      layer_norm(hc, L.ln_w[1], L.ln_b[1], xnp, nullptr, mp, st);
+      prof.run("layernorm", 0, ln_bytes, st,
+               [&] { layer_norm(hc, L.ln_w[1], L.ln_b[1], xnp, nullptr, mp, st); });
       e = EpiArgs();
       e.qu = qu.as<half>();
       e.qv = qv.as<half>();
@@ -504,42 +622,47 @@ struct BarkHip {
       e.bu = L.bu;
       e.bv = L.bv;
       e.mp = mp;
-      gemm(xnp, HIDDEN, mp, L.qkv, Epi::Qkv, e, st);
+      gemm_op("qkv_heads", xnp, HIDDEN, mp, mr, L.qkv, Epi::Qkv, e, 2.0 * 4096, st);
       e = EpiArgs();
       e.rk = rk.as<half>();
       e.pp = pp;
-      gemm(pos_rows, HIDDEN, prows, L.relk, Epi::RelK, e, st);
+      gemm_op("relk", pos_rows, HIDDEN, prows, prows, L.relk, Epi::RelK, e, 2.0 * HIDDEN, st);
       AttnArgs aa{qu.as<half>(), qv.as<half>(), kh.as<half>(), vt.as<half>(), rk.as<half>(),
                   ao.as<half>(), mp, pp, tc, tiles.as<int4>(), ntiles};
-      rel_attention(aa, st);
+      prof.run("rel_attention", attn_flops, 2.0 * mr * HIDDEN * 5 + 2.0 * prows * HIDDEN, st,
+               [&] { rel_attention(aa, st); });
       e = EpiArgs();
       e.out_f32 = hc;
       e.ldo = HIDDEN;
       e.scale = 1.0f;
-      gemm(ao.as<half>(), HIDDEN, mp, L.o, Epi::Resid, e, st);
+      gemm_op("attn_out_resid", ao.as<half>(), HIDDEN, mp, mr, L.o, Epi::Resid, e, 8.0 * HIDDEN, st);
       // ---- conv module
-      layer_norm(hc, L.ln_w[2], L.ln_b[2], xnp, nullptr, mp, st);
+      prof.run("layernorm", 0, ln_bytes, st,
+               [&] { layer_norm(hc, L.ln_w[2], L.ln_b[2], xnp, nullptr, mp, st); });
       e = EpiArgs();
       e.out_f32 = glu.as<float>();
       e.ldo = HIDDEN;
-      gemm(xnp, HIDDEN, mp, L.pw1, Epi::Glu, e, st);
-      dwconv_bn_silu(glu.as<float>(), L.dw, L.bn_a, L.bn_b, bounds.as<int2>(), xnp, mp, st);
+      gemm_op("pw1_glu", xnp, HIDDEN, mp, mr, L.pw1, Epi::Glu, e, 4.0 * HIDDEN, st);
+      prof.run("dwconv_bn_silu", 2.0 * 9 * mr * HIDDEN, (double)mr * HIDDEN * 6 + 9 * HIDDEN * 4.0, st, [&] {
+        dwconv_bn_silu(glu.as<float>(), L.dw, L.bn_a, L.bn_b, bounds.as<int2>(), xnp, mp, st);
+      });
       e = EpiArgs();
       e.out_f32 = hc;
       e.ldo = HIDDEN;
       e.scale = 1.0f;
-      gemm(xnp, HIDDEN, mp, L.pw2, Epi::Resid, e, st);
+      gemm_op("pw2_resid", xnp, HIDDEN, mp, mr, L.pw2, Epi::Resid, e, 8.0 * HIDDEN, st);
       // ---- FF2
-      layer_norm(hc, L.ln_w[3], L.ln_b[3], xnp, nullptr, mp, st);
+      prof.run("layernorm", 0, ln_bytes, st,
+               [&] { layer_norm(hc, L.ln_w[3], L.ln_b[3], xnp, nullptr, mp, st); });
       e = EpiArgs();
       e.out_f16 = hid.as<half>();
       e.ldo = FFN;
-      gemm(xnp, HIDDEN, mp, L.ff2a, Epi::Silu, e, st);
+      gemm_op("ff_up_silu", xnp, HIDDEN, mp, mr, L.ff2a, Epi::Silu, e, 2.0 * FFN, st);
       e = EpiArgs();
       e.out_f32 = hc;
       e.ldo = HIDDEN;
       e.scale = 0.5f;
-      gemm(hid.as<half>(), FFN, mp, L.ff2b, Epi::Resid, e, st);
+      gemm_op("ff_down_resid", hid.as<half>(), FFN, mp, mr, L.ff2b, Epi::Resid, e, 8.0 * HIDDEN, st);
       if (l == dump_layer) {
         ensure(dump, (size_t)mp * HIDDEN * 4);
         copy_rows_f32(hc, HIDDEN, dump.as<float>(), HIDDEN, mp, HIDDEN, st);
@@ -547,9 +670,12 @@ struct BarkHip {
       // ---- norm_out (fused with the next block's first LayerNorm)
       if (l + 1 < n_layers) {
         const DevLayer& N = layers[l + 1];
-        layer_norm2(hc, L.ln_w[4], L.ln_b[4], ha, N.ln_w[0], N.ln_b[0], xnp, mp, st);
+        prof.run("layernorm_pair", 0, (double)mr * HIDDEN * (4 + 4 + 2), st, [&] {
+          layer_norm2(hc, L.ln_w[4], L.ln_b[4], ha, N.ln_w[0], N.ln_b[0], xnp, mp, st);
+        });
       } else {
-        layer_norm(hc, L.ln_w[4], L.ln_b[4], xnp, ha, mp, st);
+        prof.run("layernorm", 0, (double)mr * HIDDEN * (4 + 4 + 2), st,
+                 [&] { layer_norm(hc, L.ln_w[4], L.ln_b[4], xnp, ha, mp, st); });
       }
       std::swap(hc, ha);
     }
@@ -557,7 +683,7 @@ struct BarkHip {
     ep.out_f32 = pooler.as<float>();
     ep.ldo = PROJ;
     ep.bias = proj_b;
-    gemm(xnp, HIDDEN, mp, proj_w, Epi::StoreF32, ep, st);
+    gemm_op("projector", xnp, HIDDEN, mp, mr, proj_w, Epi::StoreF32, ep, 4.0 * PROJ, st);
   }
 
   // Shared body of the mel-input entry points; pooler rows of sequence i are
@@ -824,6 +950,27 @@ int bark_hip_encode_mel_batch_device(BarkHip* h, const float* d_mel, const int32
     hipStream_t st = stream ? static_cast<hipStream_t>(stream) : h->stream;
     h->encode_mel_batch(d_mel, true, n_frames, n_valid, batch, t_out, d_pooler, true,
                         pooler_cap, st);
+  });
+}
+
+int bark_hip_profile(BarkHip* h, int enable) {
+  return guarded([&] {
+    BARK_REQUIRE(h, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    (void)h->prof.report();  // drop anything recorded so far
+    h->prof.on = enable != 0;
+  });
+}
+
+int bark_hip_profile_report(BarkHip* h, char* buf, size_t cap) {
+  return guarded([&] {
+    BARK_REQUIRE(h && buf && cap > 0, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    const std::string r = h->prof.report();
+    BARK_REQUIRE(r.size() + 1 <= cap, "profile report buffer too small");
+    std::memcpy(buf, r.c_str(), r.size() + 1);
   });
 }
 

@@ -1,0 +1,240 @@
+#!/usr/bin/env python
+"""Benchmark of the HIP Conformer encoder on one MI355X.
+
+Workload: the full 24-block encoder with every
+linear in the 4-bit code + per-row level-table format, batch 1, on a synthetic
+log-mel [17656, 128] (176.56 s of audio) -> T = 2207 encoder frames. One step =
+conv front end + 24 blocks + projector over that utterance, with the mel
+already resident in HBM. value = audio seconds per second (encoder RTFx).
+
+Also reported:
+  roofline     - the dominant kernel of the step, from per-launch HIP events
+                 recorded on the library's stream during the timed region;
+  gemm_lowbit  - the isolated 4-bit linear of configs[1] (bf16 activations,
+                 bf16 out) at T in {188, 2207}, rotating >256 MB of distinct
+                 codes/activations so the MALL cannot serve them;
+  cpu_baseline - the CPU oracle (C restatement of the reference CPU backend)
+                 on this host's cores over a bounded sample of the same
+                 workload, extrapolated to 24 blocks.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import importlib.util
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+FRAMES = 17656
+AUDIO_S = FRAMES * 0.01
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense f16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def load_pkg():
+    name = "bark3_wgpu_amd"
+    if name in sys.modules:
+        return sys.modules[name]
+    init = ROOT / "bark3-wgpu_amd" / "__init__.py"
+    spec = importlib.util.spec_from_file_location(name, init, submodule_search_locations=[str(init.parent)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def bench_encoder(pkg, synth, torch, steps: int, warmup: int):
+    src = synth.SynthCheckpoint(seed=0, n_layers=24, style="baseline", lowbit=True)
+    t0 = time.time()
+    enc = pkg.HipEncoder.load_with(src, device=0, n_layers=24)
+    log(f"[bench] weights loaded in {time.time() - t0:.1f}s")
+    mel = torch.from_numpy(synth.mel(FRAMES, seed=0)).cuda()
+    T = pkg.conv_len(pkg.conv_len(pkg.conv_len(FRAMES)))
+    pooler = torch.empty((T, 640), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        enc.encode_mel_batch_device(mel.data_ptr(), [FRAMES], [FRAMES], pooler.data_ptr(), pooler.numel(), stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(pooler).all()), "non-finite encoder output"
+    enc.profile(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    prof = enc.profile_report()
+    enc.profile(False)
+    log(f"[bench] encoder step {dt * 1e3:.3f} ms over {steps} steps (T={T})")
+    enc.close()
+    return dt, T, prof
+
+
+def bench_gemm(pkg, torch, T: int, K: int, N: int, reps: int = 192):
+    """Average launch time of the isolated 4-bit linear over `reps` distinct
+    buffer sets (codes + activations + outputs)."""
+    g = torch.Generator(device="cuda").manual_seed(T * 7 + K + N)
+    A = [torch.randn((T, K), device="cuda", generator=g).to(torch.bfloat16) for _ in range(reps)]
+    codes = [torch.randint(0, 256, (N, K // 2), device="cuda", dtype=torch.uint8, generator=g) for _ in range(reps)]
+    lut = [torch.sort(torch.randn((N, 16), device="cuda", generator=g) * 0.02, dim=1).values.half() for _ in range(reps)]
+    C = [torch.empty((T, N), device="cuda", dtype=torch.bfloat16) for _ in range(reps)]
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    def launch(i):
+        pkg.lowbit_linear(A[i].data_ptr(), 1, codes[i].data_ptr(), lut[i].data_ptr(), C[i].data_ptr(), 2, T, K, N, sp)
+
+    for i in range(reps):
+        launch(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        launch(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3 / reps
+    F = 2.0 * T * K * N
+    B = K * N / 2 + 32 * N + 2 * T * K + 2 * T * N
+    del A, codes, lut, C
+    torch.cuda.empty_cache()
+    return {"T": T, "K": K, "N": N, "us": t * 1e6, "tflops": F / t / 1e12, "gbs": B / t / 1e9,
+            "mfma_frac": F / t / 1e12 / PEAK_F16_TFLOPS, "hbm_frac": B / t / 1e9 / PEAK_HBM_GBS}
+
+
+def cpu_baseline(synth, blocks: int):
+    """Oracle timing on this host: front end over the full 17656-frame mel,
+    sub linear, `blocks` blocks at T=2207 and the projector; the 24-block time
+    is extrapolated from the median per-block time."""
+    sys.path.insert(0, str(ROOT))
+    import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    src = synth.SynthCheckpoint(seed=0, n_layers=blocks, style="baseline", lowbit=True)
+    enc = oracle.Encoder(src, n_layers=blocks)
+    mel = synth.mel(FRAMES, seed=0)
+    t0 = time.perf_counter()
+    sub = oracle.subsample(src, mel, threads=threads)
+    t_front = time.perf_counter() - t0
+    T = sub.shape[0]
+    sub_w = oracle.PackW(oracle.round_f16(src.read("encoder.subsampling.linear.weight")), half=True)
+    t0 = time.perf_counter()
+    x = oracle.gemm(sub, sub_w, threads=threads)
+    t_lin = time.perf_counter() - t0
+    per_block = []
+    for l in range(blocks):
+        t0 = time.perf_counter()
+        x = enc.block(l, x, threads=threads)
+        per_block.append(time.perf_counter() - t0)
+    proj_w = oracle.PackW(oracle.round_f16(src.read("encoder_projector.weight")), half=True)
+    t0 = time.perf_counter()
+    oracle.gemm(x, proj_w, threads=threads)
+    t_proj = time.perf_counter() - t0
+    t_block = float(np.median(per_block))
+    total = t_front + t_lin + 24 * t_block + t_proj
+    sample = (f"front end over {FRAMES} mel frames + sub linear + {blocks} of 24 blocks at T={T} + projector "
+              f"(measured {t_front + t_lin + sum(per_block) + t_proj:.1f} s); 24-block time = 24 x median block "
+              f"{t_block:.3f} s; total {total:.2f} s")
+    return {"value": AUDIO_S / total, "unit": "audio s/s", "cores": threads, "kind": "port", "sample": sample}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-blocks", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    pkg = load_pkg()
+    synth = importlib.import_module("bark3_wgpu_amd.synth")
+    if not torch.cuda.is_available() or pkg.lib().bark_hip_device_count() < 1:
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 1
+
+    dt, T, prof = bench_encoder(pkg, synth, torch, args.steps, args.warmup)
+    gemm_labels = {k: v for k, v in prof.items() if v["flops"] > 0 and k not in ("rel_attention", "dwconv_bn_silu",
+                                                                                 "fe_conv1", "fe_dwconv")}
+    dom = max(gemm_labels, key=lambda k: gemm_labels[k]["ms"])
+    d = prof[dom]
+    avg_s = d["ms"] / d["count"] / 1e3
+    flops_per_launch = d["flops"] / d["count"]
+    achieved = flops_per_launch / avg_s / 1e12
+    breakdown = {k: {"ms_per_step": v["ms"] / args.steps, "launches_per_step": v["count"] // args.steps,
+                     "tflops": (v["flops"] / (v["ms"] / 1e3) / 1e12) if v["flops"] else None,
+                     "gbs": v["bytes"] / (v["ms"] / 1e3) / 1e9}
+                 for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}
+    for k, v in breakdown.items():
+        log(f"[bench]   {k:16s} {v['ms_per_step']:8.3f} ms/step  x{v['launches_per_step']:<4d} "
+            f"{(v['tflops'] or 0):8.1f} TFLOP/s {v['gbs']:8.1f} GB/s")
+
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get(dom)
+
+    gemm = []
+    if not args.no_gemm:
+        for t in (188, 2207):
+            for k, n in ((1024, 4096), (4096, 1024), (1024, 3072)):
+                r = bench_gemm(pkg, torch, t, k, n)
+                gemm.append(r)
+                log(f"[bench] lowbit linear T={t} K={k} N={n}: {r['us']:.2f} us, {r['tflops']:.1f} TFLOP/s, "
+                    f"{r['gbs']:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        t0 = time.time()
+        cpu = cpu_baseline(synth, args.cpu_blocks)
+        log(f"[bench] cpu baseline {cpu['value']:.2f} audio s/s ({time.time() - t0:.1f}s)")
+
+    line = {
+        "metric": "encoder RTFx (audio s/s), 24-block 4-bit Conformer encoder, 1 GPU",
+        "value": AUDIO_S / dt,
+        "unit": "audio s/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dt * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded log-mel N(0,1); random-init weights, 4-bit codes U{0..15} + sorted N(0,0.02) f16 tables)",
+        "config": {"workload": "BASELINE configs[3]: 24-block 4-bit encoder, log-mel 17656x128 -> T=2207, batch 1",
+                   "frames": FRAMES, "T": T, "audio_s": AUDIO_S, "encoder_frames_per_s": T / dt},
+        "roofline": {"kernel": dom, "bound": "mfma", "achieved": achieved, "peak": PEAK_F16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_F16_TFLOPS, "traffic": traffic,
+                     "flops_per_launch": flops_per_launch, "avg_launch_us": avg_s * 1e6},
+        "breakdown": breakdown,
+        "gemm_lowbit": gemm,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -106,6 +106,16 @@ int bark_hip_encode_mel_batch_device(BarkHip *h, const float *d_mel, const int32
                                      const int32_t *n_valid, int32_t batch, int32_t *t_out,
                                      float *d_pooler, size_t pooler_cap, void *stream);
 
+/* Per-operator GPU timing, the counterpart of BARK3_ENC_PROFILE
+ * (src/encoder/prof.rs:1-127, src/encoder.rs:823-827): while enabled, every
+ * launch of the forward is bracketed by HIP events on its stream. Enabling or
+ * disabling discards what was recorded. */
+int bark_hip_profile(BarkHip *h, int enable);
+/* Writes JSON {label: {count, ms, flops, bytes}} aggregated over everything
+ * recorded since the last report (flops/bytes are the algorithmic work of the
+ * launches) and clears it. Synchronises with the recorded work. */
+int bark_hip_profile_report(BarkHip *h, char *buf, size_t cap);
+
 /* Isolated 4-bit level-table linear (one bm64_lb dispatch of Ctx::gemm_f32,
  * src/encoder.rs:1039-1100, in the generic table format): device pointers
  * A (T, K) activations, codes (N, K/2) bytes, lut16 (N, 16) f16, C (T, N).
