@@ -1,0 +1,128 @@
+"""Full-encoder GPU parity: every block's pre-norm residual and the pooler
+against the CPU oracle, batched packing, length masks, long streams and the
+reference's own low-bit format. Tolerance (BASELINE): relative max-abs error
+<= 1e-2 per block; the measured per-layer table is printed."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import rel_max_abs
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _per_layer(enc, orc, sub, t, n_layers, layers):
+    want_pool, want_dumps = orc.encode_dump(sub, t)
+    errs = []
+    for l in layers:
+        got = enc.encode(sub, t, dump_layer=l)
+        errs.append((l, rel_max_abs(got.block, want_dumps[l])))
+    pool = enc.encode(sub, t).pooler
+    return errs, rel_max_abs(pool, want_pool)
+
+
+def test_config2_full_encoder_t188(pkg, synth, oracle):
+    """24 blocks, bf16 weights, log-mel [1500,128] -> T=188, via
+    the conv front end; per-layer errors from encode() dumps."""
+    print("case config2 t=188", flush=True)
+    src = synth.SynthCheckpoint(seed=21, n_layers=24, style="rich")
+    mel = synth.mel(1500, seed=21)
+    with pkg.HipEncoder.load_with(src, n_layers=24) as enc:
+        pooler, t = enc.encode_mel(mel)
+        assert t == 188
+        orc = oracle.Encoder(src, 24)
+        sub = oracle.subsample(src, mel)
+        errs, e_pool_sub = _per_layer(enc, orc, sub, t, 24, range(24))
+    want = orc.encode(sub, t)
+    e_pool = rel_max_abs(pooler, want)
+    print("  per-layer rel max-abs:", " ".join(f"{l}:{e:.1e}" for l, e in errs))
+    print(f"  pooler (mel path) {e_pool:.2e}, pooler (sub path) {e_pool_sub:.2e}")
+    assert max(e for _, e in errs) <= TOL
+    assert e_pool <= TOL and e_pool_sub <= TOL
+
+
+def test_config3_lowbit_t2207(pkg, synth, oracle):
+    """24 blocks with 4-bit linears, log-mel [17656,128] -> T=2207."""
+    print("case config3 t=2207", flush=True)
+    src = synth.SynthCheckpoint(seed=31, n_layers=24, style="rich", lowbit=True)
+    mel = synth.mel(17656, seed=31)
+    with pkg.HipEncoder.load_with(src, n_layers=24) as enc:
+        pooler, t = enc.encode_mel(mel)
+        assert t == 2207
+        orc = oracle.Encoder(src, 24)
+        sub = oracle.subsample(src, mel)
+        want_pool, want_dumps = orc.encode_dump(sub, t)
+        errs = [(l, rel_max_abs(enc.encode(sub, t, dump_layer=l).block, want_dumps[l])) for l in (0, 1, 11, 23)]
+    e_pool = rel_max_abs(pooler, want_pool)
+    print("  per-layer rel max-abs:", " ".join(f"{l}:{e:.1e}" for l, e in errs), f" pooler {e_pool:.2e}")
+    assert max(e for _, e in errs) <= TOL and e_pool <= TOL
+
+
+def test_batch_equals_individual(pkg, synth):
+    """configs[4] semantics: each utterance of a packed batch equals its own
+    batch-1 run (identical per-row arithmetic, so the match is exact)."""
+    rng = np.random.default_rng(41)
+    frames = [int(x) for x in rng.integers(500, 3000, size=5)]
+    print(f"case batch frames={frames}", flush=True)
+    src = synth.SynthCheckpoint(seed=41, n_layers=2, style="rich", lowbit=True)
+    mels = [synth.mel(f, seed=i) for i, f in enumerate(frames)]
+    with pkg.HipEncoder.load_with(src, n_layers=2) as enc:
+        batch = enc.encode_mel_batch(mels)
+        singles = [enc.encode_mel(m)[0] for m in mels]
+    for b, s in zip(batch, singles):
+        assert b.shape == s.shape
+        assert np.array_equal(b, s)
+
+
+def test_n_valid_masks_front_end(pkg, synth, oracle):
+    """n_valid < n_frames zeroes the masked frames after each strided conv
+    (src/sub.rs:259-273)."""
+    src = synth.SynthCheckpoint(seed=51, n_layers=1, style="rich")
+    mel = synth.mel(800, seed=51)
+    with pkg.HipEncoder.load_with(src, n_layers=1) as enc:
+        got, t = enc.encode_mel(mel, n_valid=523)
+    sub = oracle.subsample(src, mel, n_valid=523)
+    want = oracle.Encoder(src, 1).encode(sub, t)
+    err = rel_max_abs(got, want)
+    print(f"case n_valid=523 of 800: pooler err {err:.2e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("t", [4096, 15000])
+def test_long_stream_one_block(pkg, synth, oracle, t):
+    """Past the reference's 4096-frame fused-softmax limit and the 20-minute
+    stream of configs[4] (T=15000): flash attention keeps O(T) memory."""
+    print(f"case long stream t={t}", flush=True)
+    src = synth.SynthCheckpoint(seed=61, n_layers=1, style="rich", lowbit=True)
+    sub = np.random.default_rng([t, 61]).standard_normal((t, 4096), dtype=np.float32)
+    with pkg.HipEncoder.load_with(src, n_layers=1, front_end=False) as enc:
+        got = enc.encode(sub, t, dump_layer=0)
+    want_pool, want_dumps = oracle.Encoder(src, 1).encode_dump(sub, t)
+    e_blk, e_pool = rel_max_abs(got.block, want_dumps[0]), rel_max_abs(got.pooler, want_pool)
+    print(f"  block err {e_blk:.2e} pooler err {e_pool:.2e}")
+    assert e_blk <= TOL and e_pool <= TOL
+
+
+def test_reference_lowbit_format_equals_f16(pkg, synth):
+    """The reference's LowBitTensor path (codes in 0..2k, k levels per row)
+    gives bit-identical results to f16 weights holding the expanded values —
+    the invariant of the reference's `lbtest` (src/diagnostics/gemm.rs:538-652)."""
+    low = synth.SynthCheckpoint(seed=71, n_layers=1, style="rich", lowbit=True, lowbit_format="levels", k_lev=3)
+
+    class Expanded:
+        def read(self, name):
+            v = low.read(name)
+            return v.astype(np.float16) if low.read_lowbit(name) is not None else v
+
+        def read_lowbit(self, name):
+            return None
+
+    sub = np.random.default_rng(71).standard_normal((200, 4096), dtype=np.float32)
+    with pkg.HipEncoder.load_with(low, n_layers=1, front_end=False) as a:
+        ya = a.encode(sub, 200, dump_layer=0)
+    with pkg.HipEncoder.load_with(Expanded(), n_layers=1, front_end=False) as b:
+        yb = b.encode(sub, 200, dump_layer=0)
+    assert np.array_equal(ya.pooler, yb.pooler) and np.array_equal(ya.block, yb.block)
