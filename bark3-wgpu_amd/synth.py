@@ -5,6 +5,10 @@ A `SynthCheckpoint` behaves like the reference's `WeightSource`
 (what `RawTensor::to_f32` yields for a bf16 checkpoint) and `read_lowbit(name)`
 returns the 4-bit form of a linear weight, or None.
 
+attn_std scales q/k/relative_k projections and bias_u/bias_v (default 0.02,
+like every other weight); golden fixtures raise it so that attention is sharp
+and its position term dominates.
+
 Styles:
   "baseline" - the BASELINE.json configs literally: every weight N(0, 0.02)
                stored as bf16, LayerNorm 1/0, BatchNorm mean 0 var 1 w 1 b 0,
@@ -80,9 +84,9 @@ def is_linear(name: str) -> bool:
 
 class SynthCheckpoint:
     def __init__(self, seed: int = 0, n_layers: int = 24, style: str = "rich", lowbit: bool = False,
-                 lowbit_format: str = "lut16", k_lev: int = 2):
+                 lowbit_format: str = "lut16", k_lev: int = 2, attn_std: float = 0.02):
         assert style in ("rich", "baseline") and lowbit_format in ("lut16", "levels")
-        self.seed, self.n_layers, self.style = seed, n_layers, style
+        self.seed, self.n_layers, self.style, self.attn_std = seed, n_layers, style, attn_std
         self.lowbit, self.lowbit_format, self.k_lev = lowbit, lowbit_format, k_lev
 
     def _rng(self, name: str, salt: int = 0) -> np.random.Generator:
@@ -128,6 +132,8 @@ class SynthCheckpoint:
             v = rng.standard_normal(n, dtype=np.float32) * 0.02 if rich else np.zeros(n, np.float32)
         else:
             std = 0.02
+            if any(k in name for k in ("q_proj", "k_proj", "relative_k_proj", "bias_u", "bias_v")):
+                std = self.attn_std  # larger values make attention peaky and position-sensitive
             if rich and name.startswith("encoder.subsampling.layers."):
                 std = 1.0 / 3.0 if shp[1] == 1 else 1.0 / 16.0
             v = rng.standard_normal(n, dtype=np.float32) * std
