@@ -288,7 +288,11 @@ struct BarkHip {
     g.n = L.rows;
     g.k = L.cols;
     if (L.lut4) {
-      g.codes = upload(L.codes.data(), L.codes.size());
+      BARK_REQUIRE(L.cols % 64 == 0, "4-bit weights need a multiple of 64 columns");
+      std::vector<uint8_t> sw = L.codes;
+      swizzle_codes(sw.data(), sw.size());
+      g.codes = upload(sw.data(), sw.size());
+      g.swizzled = true;
       g.lut = reinterpret_cast<const half*>(upload(L.lut.data(), L.lut.size()));
     } else {
       g.w16 = reinterpret_cast<const half*>(upload(L.w16.data(), L.w16.size()));
@@ -609,8 +613,7 @@ struct BarkHip {
       e = EpiArgs();
       e.out_f32 = hc;
       e.ldo = HIDDEN;
-      e.scale = 0.5f;
-      gemm_op("ff_down_resid", hid.as<half>(), FFN, mp, mr, L.ff1b, Epi::Resid, e, 8.0 * HIDDEN, st);
+      gemm_op("ff_down_resid", hid.as<half>(), FFN, mp, mr, L.ff1b, Epi::ResidHalf, e, 8.0 * HIDDEN, st);
       // ---- attention
       prof.run("layernorm", 0, ln_bytes, st,
                [&] { layer_norm(hc, L.ln_w[1], L.ln_b[1], xnp, nullptr, mp, st); });
@@ -661,8 +664,7 @@ struct BarkHip {
       e = EpiArgs();
       e.out_f32 = hc;
       e.ldo = HIDDEN;
-      e.scale = 0.5f;
-      gemm_op("ff_down_resid", hid.as<half>(), FFN, mp, mr, L.ff2b, Epi::Resid, e, 8.0 * HIDDEN, st);
+      gemm_op("ff_down_resid", hid.as<half>(), FFN, mp, mr, L.ff2b, Epi::ResidHalf, e, 8.0 * HIDDEN, st);
       if (l == dump_layer) {
         ensure(dump, (size_t)mp * HIDDEN * 4);
         copy_rows_f32(hc, HIDDEN, dump.as<float>(), HIDDEN, mp, HIDDEN, st);

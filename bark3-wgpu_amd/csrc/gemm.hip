@@ -14,10 +14,19 @@
 // BK = 64; each wave owns a (BM/2) x 64 patch made of 32x32 MFMA blocks.
 // A and B tiles are staged through LDS (double-buffered, rows padded by 16 B so
 // the 16-byte fragment reads of 8 lanes hit disjoint banks). In LUT4 mode each
-// thread streams 16 bytes of codes (32 weights of one row) per k-tile with one
-// coalesced load, expands them through the row's table (held in LDS) and
-// writes the f16 values into the B tile, so every weight is expanded once per
-// workgroup and reused by all BM rows.
+// thread owns one weight row for the whole kernel: its 16-entry f16 table sits
+// in 8 VGPRs as low-byte and high-byte planes, and every k-tile it streams 16
+// bytes of codes (32 weights) with one coalesced load and expands them with
+// byte permutes (v_perm_b32) — no LDS lookups — into the f16 B tile, so every
+// weight is expanded once per workgroup and reused by all BM rows.
+//
+// Code layouts: "plain" = two codes per byte, low nibble = even k (the
+// reference's layout); "swizzled" = within each 4-byte group of 8 codes, byte i
+// holds codes i (low nibble) and i+4 (high nibble), which the expansion turns
+// into natural k order with half the permutes. Encoder weights are swizzled
+// once at load.
+#include <cstdlib>
+
 #include "kernels.h"
 
 namespace bark {
@@ -37,6 +46,61 @@ struct GemmParams {
   EpiArgs ea;
 };
 
+__device__ inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Row table as byte planes: L[q] holds the low bytes of entries 4q..4q+3,
+// H[q] the high bytes.
+struct RowLut {
+  uint32_t L[4], H[4];
+};
+
+__device__ inline RowLut load_row_lut(const half* lut_row) {
+  const uint4 a = *reinterpret_cast<const uint4*>(lut_row);
+  const uint4 b = *reinterpret_cast<const uint4*>(lut_row + 8);
+  const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  RowLut t;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    t.L[q] = perm(d[2 * q + 1], d[2 * q], 0x06040200u);
+    t.H[q] = perm(d[2 * q + 1], d[2 * q], 0x07050301u);
+  }
+  return t;
+}
+
+// Four codes (one per byte of x, values 0..15) -> low and high bytes of their
+// table entries.
+__device__ inline void lookup4(uint32_t x, const RowLut& t, uint32_t& lo, uint32_t& hi) {
+  const uint32_t s7 = x & 0x07070707u;
+  const uint32_t la = perm(t.L[1], t.L[0], s7), lb = perm(t.L[3], t.L[2], s7);
+  const uint32_t ha = perm(t.H[1], t.H[0], s7), hb = perm(t.H[3], t.H[2], s7);
+  const uint32_t ms = ((x >> 1) & 0x04040404u) | 0x03020100u;  // byte i: i, or i+4 if code >= 8
+  lo = perm(lb, la, ms);
+  hi = perm(hb, ha, ms);
+}
+
+// One u32 of codes (8 consecutive k) -> 8 f16 in natural k order.
+template <bool SWZ>
+__device__ inline uint4 expand8(uint32_t w, const RowLut& t) {
+  uint32_t le, he, lo_, ho;
+  lookup4(w & 0x0F0F0F0Fu, t, le, he);
+  lookup4((w >> 4) & 0x0F0F0F0Fu, t, lo_, ho);
+  if constexpr (SWZ) {  // le/he: k 0..3, lo_/ho: k 4..7
+    return uint4{perm(he, le, 0x05010400u), perm(he, le, 0x07030602u), perm(ho, lo_, 0x05010400u),
+                 perm(ho, lo_, 0x07030602u)};
+  } else {  // le/he: k 0,2,4,6, lo_/ho: k 1,3,5,7
+    const uint32_t e01 = perm(he, le, 0x05010400u), e23 = perm(he, le, 0x07030602u);
+    const uint32_t o01 = perm(ho, lo_, 0x05010400u), o23 = perm(ho, lo_, 0x07030602u);
+    return uint4{perm(o01, e01, 0x05040100u), perm(o01, e01, 0x07060302u), perm(o23, e23, 0x05040100u),
+                 perm(o23, e23, 0x07060302u)};
+  }
+}
+
+__device__ inline float fast_sigmoid_mul(float a, float g) {
+  return a * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+
 template <int EPI>
 __device__ inline void store_one(const EpiArgs& ea, int r, int c, float v) {
   if constexpr (EPI == (int)Epi::StoreF32) {
@@ -51,10 +115,13 @@ __device__ inline void store_one(const EpiArgs& ea, int r, int c, float v) {
     u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite inputs)
     reinterpret_cast<uint16_t*>(ea.out_f16)[(size_t)r * ea.ldo + c] = (uint16_t)(u >> 16);
   } else if constexpr (EPI == (int)Epi::Silu) {
-    ea.out_f16[(size_t)r * ea.ldo + c] = (half)silu(v);
+    ea.out_f16[(size_t)r * ea.ldo + c] = (half)fast_sigmoid_mul(v, v);
   } else if constexpr (EPI == (int)Epi::Resid) {
     float* p = ea.out_f32 + (size_t)r * ea.ldo + c;
     *p = *p + ea.scale * v;
+  } else if constexpr (EPI == (int)Epi::ResidHalf) {
+    float* p = ea.out_f32 + (size_t)r * ea.ldo + c;
+    *p = *p + 0.5f * v;
   } else if constexpr (EPI == (int)Epi::Qkv) {
     const int which = c >> 10, hd = c & 1023, h = hd >> 7, d = hd & 127;
     const size_t hr = ((size_t)h * ea.mp + r) * HDIM + d;
@@ -79,7 +146,7 @@ __device__ inline void store_one(const EpiArgs& ea, int r, int c, float v) {
   }
 }
 
-template <int BM, bool LUT4, bool ABF16, int EPI>
+template <int BM, bool LUT4, bool SWZ, bool ABF16, int EPI>
 __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
   constexpr int WTM = BM / 2;       // wave tile rows
   constexpr int FM = WTM / 32;      // 32-row MFMA blocks per wave
@@ -89,50 +156,52 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
 
   __shared__ __attribute__((aligned(16))) half As[2][BM * LDK];
   __shared__ __attribute__((aligned(16))) half Bs[2][BN * LDK];
-  __shared__ __attribute__((aligned(16))) half lut_s[LUT4 ? BN * 16 : 8];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int wm = wid >> 1, wn = wid & 1;
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
   const int l32 = lane & 31, lhi = lane >> 5;
 
-  uint4 a_reg[A_CH];
-  uint4 b_reg[LUT4 ? 1 : B_CH];
+  // Four register stages hold the k-tiles in flight from global memory: a
+  // tile's loads are issued three iterations of MFMA work before its LDS
+  // store, which covers HBM latency.
+  struct Stage {
+    uint4 a[A_CH];
+    uint4 b[LUT4 ? 1 : B_CH];
+  };
+  Stage r0, r1, r2, r3;
 
-  if constexpr (LUT4) {
-    // 128 rows x 16 halves = 256 chunks of 16 B: one per thread.
-    const uint4* src = reinterpret_cast<const uint4*>(p.lut + (size_t)n0 * 16);
-    reinterpret_cast<uint4*>(lut_s)[tid] = src[tid];
-  }
+  RowLut lut;  // this thread's weight row: n0 + tid/2
+  if constexpr (LUT4) lut = load_row_lut(p.lut + (size_t)(n0 + (tid >> 1)) * 16);
 
-  auto load_tiles = [&](int kt) {
+  auto load_tiles = [&](int kt, Stage& st) {
     const int k0 = kt * BK;
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int ch = tid + 256 * i, row = ch >> 3, col = (ch & 7) * 8;
-      a_reg[i] = (m0 + row < p.M)
-                     ? *reinterpret_cast<const uint4*>(p.A + (size_t)(m0 + row) * p.lda + k0 + col)
-                     : uint4{0u, 0u, 0u, 0u};
+      st.a[i] = (m0 + row < p.M)
+                    ? *reinterpret_cast<const uint4*>(p.A + (size_t)(m0 + row) * p.lda + k0 + col)
+                    : uint4{0u, 0u, 0u, 0u};
     }
     if constexpr (LUT4) {
       const int row = tid >> 1, part = tid & 1;
-      b_reg[0] = *reinterpret_cast<const uint4*>(p.codes + (size_t)(n0 + row) * (p.K >> 1) +
-                                                 (k0 >> 1) + part * 16);
+      st.b[0] = *reinterpret_cast<const uint4*>(p.codes + (size_t)(n0 + row) * (p.K >> 1) +
+                                                (k0 >> 1) + part * 16);
     } else {
 #pragma unroll
       for (int i = 0; i < B_CH; ++i) {
         const int ch = tid + 256 * i, row = ch >> 3, col = (ch & 7) * 8;
-        b_reg[i] = *reinterpret_cast<const uint4*>(p.W + (size_t)(n0 + row) * p.K + k0 + col);
+        st.b[i] = *reinterpret_cast<const uint4*>(p.W + (size_t)(n0 + row) * p.K + k0 + col);
       }
     }
   };
 
-  auto store_tiles = [&](int stage) {
+  auto store_tiles = [&](int stage, const Stage& st) {
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int ch = tid + 256 * i, row = ch >> 3, col = (ch & 7) * 8;
       if constexpr (ABF16) {  // bf16 -> f16: exact for |x| in the f16 normal range
-        const uint32_t w4[4] = {a_reg[i].x, a_reg[i].y, a_reg[i].z, a_reg[i].w};
+        const uint32_t w4[4] = {st.a[i].x, st.a[i].y, st.a[i].z, st.a[i].w};
         half8 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -141,26 +210,20 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
         }
         st_half8(&As[stage][row * LDK + col], v);
       } else {
-        *reinterpret_cast<uint4*>(&As[stage][row * LDK + col]) = a_reg[i];
+        *reinterpret_cast<uint4*>(&As[stage][row * LDK + col]) = st.a[i];
       }
     }
     if constexpr (LUT4) {
       const int row = tid >> 1, part = tid & 1;
-      const half* tb = lut_s + row * 16;
-      const uint32_t w4[4] = {b_reg[0].x, b_reg[0].y, b_reg[0].z, b_reg[0].w};
+      const uint32_t w4[4] = {st.b[0].x, st.b[0].y, st.b[0].z, st.b[0].w};
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t w = w4[q];  // 8 codes, low nibble first = ascending k
-        half8 v;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = tb[(w >> (4 * e)) & 15u];
-        st_half8(&Bs[stage][row * LDK + part * 32 + q * 8], v);
-      }
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<uint4*>(&Bs[stage][row * LDK + part * 32 + q * 8]) = expand8<SWZ>(w4[q], lut);
     } else {
 #pragma unroll
       for (int i = 0; i < B_CH; ++i) {
         const int ch = tid + 256 * i, row = ch >> 3, col = (ch & 7) * 8;
-        *reinterpret_cast<uint4*>(&Bs[stage][row * LDK + col]) = b_reg[i];
+        *reinterpret_cast<uint4*>(&Bs[stage][row * LDK + col]) = st.b[i];
       }
     }
   };
@@ -173,15 +236,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const int nk = p.K / BK;
-  load_tiles(0);
-  if constexpr (LUT4) __syncthreads();  // lut_s visible before expansion
-  store_tiles(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) load_tiles(kt + 1);
+  auto compute = [&](int cur) {
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       half8 af[FM], bf[FN];
@@ -197,9 +252,99 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
-    if (kt + 1 < nk) store_tiles(cur ^ 1);
+  };
+
+  // One k-tile of MFMAs from LDS stage `cur`, fused with writing the next
+  // k-tile (register stage `st`) into LDS stage `nxt`: each 16-k slice issues
+  // its fragment reads, expands one code word of the next tile (VALU) and
+  // stores it, and runs its MFMAs, so the matrix cores keep working while the
+  // codes are expanded. Scheduler groups keep that order per slice.
+  auto step = [&](int cur, int nxt, const Stage& st) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int ch = tid + 256 * i, row = ch >> 3, col = (ch & 7) * 8;
+      if constexpr (ABF16) {
+        const uint32_t w4[4] = {st.a[i].x, st.a[i].y, st.a[i].z, st.a[i].w};
+        half8 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[2 * e] = (half)__uint_as_float(w4[e] << 16);
+          v[2 * e + 1] = (half)__uint_as_float(w4[e] & 0xffff0000u);
+        }
+        st_half8(&As[nxt][row * LDK + col], v);
+      } else {
+        *reinterpret_cast<uint4*>(&As[nxt][row * LDK + col]) = st.a[i];
+      }
+    }
+    const int brow = tid >> 1, bpart = tid & 1;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      half8 af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = ld_half8(&As[cur][(wm * WTM + i * 32 + l32) * LDK + ks * 16 + lhi * 8]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bf[j] = ld_half8(&Bs[cur][(wn * 64 + j * 32 + l32) * LDK + ks * 16 + lhi * 8]);
+      if constexpr (LUT4) {
+        const uint32_t w = ks == 0 ? st.b[0].x : ks == 1 ? st.b[0].y : ks == 2 ? st.b[0].z : st.b[0].w;
+        const uint4 q = expand8<SWZ>(w, lut);
+        *reinterpret_cast<uint4*>(&Bs[nxt][brow * LDK + bpart * 32 + ks * 8]) = q;
+      } else {
+#pragma unroll
+        for (int i = ks * B_CH / 4; i < (ks + 1) * B_CH / 4; ++i) {
+          const int ch = tid + 256 * i, row = ch >> 3, col = (ch & 7) * 8;
+          *reinterpret_cast<uint4*>(&Bs[nxt][row * LDK + col]) = st.b[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      constexpr int VPER = LUT4 ? (26 + FM * FN - 1) / (FM * FN) : 1;
+      __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
+#pragma unroll
+      for (int m = 0; m < FM * FN; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, VPER, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    }
+  };
+
+  // K is a multiple of 4*BK: the loop runs in branch-free groups of four
+  // k-tiles. At the top of each group LDS stage 0 holds tile kt and register
+  // stages r1..r3 hold tiles kt+1..kt+3; each step computes one tile, stores the
+  // next one into the other LDS stage and refills the register stage it freed.
+  const int nk = p.K / BK;
+  load_tiles(0, r0);
+  load_tiles(1, r1);
+  load_tiles(2, r2);
+  load_tiles(3, r3);
+  store_tiles(0, r0);
+  __syncthreads();
+  for (int kt = 0; kt + 4 < nk; kt += 4) {
+    load_tiles(kt + 4, r0);
+    step(0, 1, r1);
+    __syncthreads();
+    load_tiles(kt + 5, r1);
+    step(1, 0, r2);
+    __syncthreads();
+    load_tiles(kt + 6, r2);
+    step(0, 1, r3);
+    __syncthreads();
+    load_tiles(kt + 7, r3);
+    step(1, 0, r0);
     __syncthreads();
   }
+  step(0, 1, r1);
+  __syncthreads();
+  step(1, 0, r2);
+  __syncthreads();
+  step(0, 1, r3);
+  __syncthreads();
+  compute(1);
 
   // Epilogue. Accumulator element v of lane `lane` in block (i, j) is
   // row 8*(v/4) + 4*(lane/32) + v%4, column lane%32 of that 32x32 block.
@@ -215,7 +360,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
         const int r = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
         if (r >= p.M) continue;
         const float a = acc[i][0][v], g = acc[i][1][v];
-        ea.out_f32[(size_t)r * ea.ldo + c] = a / (1.0f + __expf(-g));
+        ea.out_f32[(size_t)r * ea.ldo + c] = fast_sigmoid_mul(a, g);
       }
   } else {
 #pragma unroll
@@ -231,35 +376,21 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
   }
 }
 
-template <int BM, bool LUT4>
-void launch_bm(const GemmParams& p, Epi epi, bool abf16, hipStream_t s) {
+// Full epilogue set: f16 weights and swizzled 4-bit weights (the encoder).
+template <int BM, bool LUT4, bool SWZ>
+void launch_full(const GemmParams& p, Epi epi, hipStream_t s) {
   dim3 grid(p.N / BN, ceil_div(p.M, BM)), block(256);
-  if (abf16) {
-    switch (epi) {
-      case Epi::StoreF32:
-        hipLaunchKernelGGL((gemm_kernel<BM, LUT4, true, (int)Epi::StoreF32>), grid, block, 0, s, p);
-        break;
-      case Epi::StoreF16:
-        hipLaunchKernelGGL((gemm_kernel<BM, LUT4, true, (int)Epi::StoreF16>), grid, block, 0, s, p);
-        break;
-      case Epi::StoreBF16:
-        hipLaunchKernelGGL((gemm_kernel<BM, LUT4, true, (int)Epi::StoreBF16>), grid, block, 0, s, p);
-        break;
-      default:
-        throw Error{"gemm: bf16 activations support plain stores only"};
-    }
-    return;
-  }
   switch (epi) {
-#define BARK_CASE(E)                                                                    \
-  case Epi::E:                                                                          \
-    hipLaunchKernelGGL((gemm_kernel<BM, LUT4, false, (int)Epi::E>), grid, block, 0, s, p); \
+#define BARK_CASE(E)                                                                          \
+  case Epi::E:                                                                                \
+    hipLaunchKernelGGL((gemm_kernel<BM, LUT4, SWZ, false, (int)Epi::E>), grid, block, 0, s, p); \
     break;
     BARK_CASE(StoreF32)
     BARK_CASE(StoreF16)
     BARK_CASE(StoreBF16)
     BARK_CASE(Silu)
     BARK_CASE(Resid)
+    BARK_CASE(ResidHalf)
     BARK_CASE(Glu)
     BARK_CASE(Qkv)
     BARK_CASE(RelK)
@@ -269,26 +400,79 @@ void launch_bm(const GemmParams& p, Epi epi, bool abf16, hipStream_t s) {
   }
 }
 
+// Plain-layout 4-bit weights (the isolated linear): plain stores, f16 or bf16 A.
+template <int BM>
+void launch_plain(const GemmParams& p, Epi epi, bool abf16, hipStream_t s) {
+  dim3 grid(p.N / BN, ceil_div(p.M, BM)), block(256);
+#define BARK_CASE(E)                                                                              \
+  case Epi::E:                                                                                    \
+    if (abf16)                                                                                    \
+      hipLaunchKernelGGL((gemm_kernel<BM, true, false, true, (int)Epi::E>), grid, block, 0, s, p);  \
+    else                                                                                          \
+      hipLaunchKernelGGL((gemm_kernel<BM, true, false, false, (int)Epi::E>), grid, block, 0, s, p); \
+    break;
+  switch (epi) {
+    BARK_CASE(StoreF32)
+    BARK_CASE(StoreF16)
+    BARK_CASE(StoreBF16)
+    default:
+      throw Error{"gemm: plain-layout 4-bit weights support plain stores only"};
+  }
+#undef BARK_CASE
+}
+
+// Rows per workgroup tile: the largest tile height that still gives every CU
+// at least one workgroup (tiles this small in count leave CUs idle, which no
+// per-tile efficiency makes up for). BARK_HIP_GEMM_BM forces a height (tuning).
+int pick_bm(int M, int N) {
+  static const int forced = [] {
+    const char* e = getenv("BARK_HIP_GEMM_BM");
+    return e ? atoi(e) : 0;
+  }();
+  if (forced == 64 || forced == 128 || forced == 256) return forced;
+  const int cus = 256;
+  for (int bm : {256, 128}) {
+    const long tiles = (long)ceil_div(M, bm) * (N / BN);
+    if (tiles >= cus) return bm;
+  }
+  return 64;
+}
+
 }  // namespace
+
+void swizzle_codes(uint8_t* codes, size_t nbytes) {
+  // plain byte j of a 4-byte group = n(2j) | n(2j+1) << 4; swizzled byte i = n(i) | n(i+4) << 4
+  for (size_t g = 0; g + 4 <= nbytes; g += 4) {
+    uint8_t n[8];
+    for (int j = 0; j < 4; ++j) {
+      n[2 * j] = codes[g + j] & 15;
+      n[2 * j + 1] = codes[g + j] >> 4;
+    }
+    for (int i = 0; i < 4; ++i) codes[g + i] = (uint8_t)(n[i] | (n[i + 4] << 4));
+  }
+}
 
 void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const EpiArgs& ea,
           hipStream_t stream, bool a_bf16) {
   BARK_REQUIRE(A != nullptr, "gemm: null A");
-  BARK_REQUIRE(W.k % BK == 0 && W.k > 0, "gemm: K must be a positive multiple of 64");
+  BARK_REQUIRE(W.k % (4 * BK) == 0 && W.k > 0, "gemm: K must be a positive multiple of 256");
   BARK_REQUIRE(W.n % BN == 0 && W.n > 0, "gemm: N must be a positive multiple of 128");
   BARK_REQUIRE(M > 0, "gemm: M must be positive");
   BARK_REQUIRE(lda >= W.k && lda % 8 == 0, "gemm: lda must be >= K and a multiple of 8");
   BARK_REQUIRE(W.lut4() ? (W.lut != nullptr) : (W.w16 != nullptr), "gemm: weight not set");
   GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea};
-  // Wide tiles when they still give about one workgroup per CU.
-  const bool big = (long)ceil_div(M, 128) * (W.n / BN) >= 192;
-  if (W.lut4()) {
-    if (big) launch_bm<128, true>(p, epi, a_bf16, stream);
-    else launch_bm<64, true>(p, epi, a_bf16, stream);
-  } else {
-    if (big) launch_bm<128, false>(p, epi, a_bf16, stream);
-    else launch_bm<64, false>(p, epi, a_bf16, stream);
+  const int bm = pick_bm(M, W.n);
+  BARK_REQUIRE(!a_bf16 || (W.lut4() && !W.swizzled), "gemm: bf16 activations need plain 4-bit weights");
+#define BARK_BM(BMV)                                             \
+  if (bm == BMV) {                                               \
+    if (!W.lut4()) launch_full<BMV, false, false>(p, epi, stream); \
+    else if (W.swizzled) launch_full<BMV, true, true>(p, epi, stream); \
+    else launch_plain<BMV>(p, epi, a_bf16, stream);              \
   }
+  BARK_BM(256)
+  BARK_BM(128)
+  BARK_BM(64)
+#undef BARK_BM
   BARK_HIP_CHECK(hipGetLastError());
 }
 

@@ -21,7 +21,8 @@ enum class Epi : int {
   RelK = 6,          // rk[h][r][d] = f16(v)
   BiasReluF16 = 7,   // out_f16[r][c] = f16(max(v + bias[c], 0))
   FlattenReluF16 = 8, // pixel r = (t, m): out_f16[t][c*16+m] = f16(max(v+bias[c],0))
-  StoreBF16 = 9       // out (bf16 bits in out_f16)[r][c] = bf16(v (+ bias[c]))
+  StoreBF16 = 9,      // out (bf16 bits in out_f16)[r][c] = bf16(v (+ bias[c]))
+  ResidHalf = 10      // out_f32[r][c] += 0.5 * v (the FFN half-step residual)
 };
 
 struct GemmWeight {
@@ -29,6 +30,7 @@ struct GemmWeight {
   const half* w16 = nullptr;     // (n, k) f16
   const uint8_t* codes = nullptr;  // (n, k/2) bytes, low nibble = even k
   const half* lut = nullptr;     // (n, 16) f16
+  bool swizzled = false;  // codes in the swizzled nibble order (see gemm.hip)
   int n = 0, k = 0;
   bool lut4() const { return codes != nullptr; }
 };
@@ -47,6 +49,10 @@ struct EpiArgs {
   half* rk = nullptr;
   int pp = 0;  // rows of rk per head
 };
+
+// Reorders 4-bit codes (rows x k/2 bytes, plain layout) into the swizzled
+// layout the GEMM expands with fewer permutes. Host-side, in place.
+void swizzle_codes(uint8_t* codes, size_t nbytes);
 
 // Rows >= M of A read as zero and are not stored. a_bf16: A holds bf16 bits
 // (converted to f16 while staging; exact for |a| in the f16 normal range).

@@ -120,7 +120,7 @@ int bark_hip_profile_report(BarkHip *h, char *buf, size_t cap);
  * src/encoder.rs:1039-1100, in the generic table format): device pointers
  * A (T, K) activations, codes (N, K/2) bytes, lut16 (N, 16) f16, C (T, N).
  * a_dtype: 0 = f16, 1 = bf16. c_dtype: 0 = f32, 1 = f16, 2 = bf16.
- * K % 64 == 0, N % 128 == 0. Queued on `stream`, not synchronised. */
+ * K % 256 == 0, N % 128 == 0. Queued on `stream`, not synchronised. */
 int bark_hip_lowbit_linear(const void *A, int32_t a_dtype, const uint8_t *codes,
                            const uint16_t *lut16, void *C, int32_t c_dtype, int32_t T,
                            int32_t K, int32_t N, void *stream);

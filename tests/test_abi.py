@@ -71,4 +71,4 @@ def test_bad_arguments_return_codes(pkg):
     # shape checks happen before any device access
     rc = L.bark_hip_lowbit_linear(zero.ctypes.data, 0, zero.ctypes.data, zero.ctypes.data, zero.ctypes.data, 0, 1,
                                   100, 128, None)
-    assert rc == -1 and b"multiple of 64" in L.bark_hip_last_error()
+    assert rc == -1 and b"multiple of 256" in L.bark_hip_last_error()
