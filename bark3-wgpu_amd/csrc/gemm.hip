@@ -421,21 +421,18 @@ void launch_plain(const GemmParams& p, Epi epi, bool abf16, hipStream_t s) {
 #undef BARK_CASE
 }
 
-// Rows per workgroup tile: the largest tile height that still gives every CU
-// at least one workgroup (tiles this small in count leave CUs idle, which no
-// per-tile efficiency makes up for). BARK_HIP_GEMM_BM forces a height (tuning).
+// Rows per workgroup tile, from a sweep of the encoder shapes on MI355X: 128
+// rows when that still gives every CU a workgroup (N = 2048/3072, or long
+// sequences), otherwise 64 (N = 1024 leaves CUs idle at 128 rows; at N = 4096
+// the 64-row tile was marginally faster). BARK_HIP_GEMM_BM forces a height.
 int pick_bm(int M, int N) {
   static const int forced = [] {
     const char* e = getenv("BARK_HIP_GEMM_BM");
     return e ? atoi(e) : 0;
   }();
   if (forced == 64 || forced == 128 || forced == 256) return forced;
-  const int cus = 256;
-  for (int bm : {256, 128}) {
-    const long tiles = (long)ceil_div(M, bm) * (N / BN);
-    if (tiles >= cus) return bm;
-  }
-  return 64;
+  const long tiles128 = (long)ceil_div(M, 128) * (N / BN);
+  return (tiles128 >= 256 && N < 4096) ? 128 : 64;
 }
 
 }  // namespace
