@@ -7,17 +7,23 @@
 // rel-shift/softmax + AV GEMM (src/encoder.rs:2238-2347,
 // src/encoder/shader_sources.rs:472-539; CPU: src/cpu/layer.rs:251-294,
 // src/cpu/ops.rs:133-189) without any T x T buffer: the softmax is computed
-// online over 64-key tiles.
+// online over 64-key tiles. q+u and q+v arrive pre-multiplied by
+// scale*log2(e) (qkv GEMM epilogue), so scores are already in the log2 domain.
 //
-// Work split: one workgroup = 128 queries of one (sequence, head); 4 waves,
-// each owning 32 queries. Scores are computed transposed (S^T = K . Qu^T), so
-// a lane's accumulator column is one query: the softmax max/sum need only one
-// cross-lane exchange (lane ^ 32), and the exp'd scores are already laid out
-// as the B operand of the P.V MFMA (keys permuted consistently with the V^T
-// fragment). The position term is computed as a band product
-// relK[jband] . Qv^T (96 positions x 32 queries per wave, 1.5x the in-band
-// work), written to a per-wave LDS scratch and read back along the diagonal
-// j = k + 31 - q_local — that read is the rel-shift.
+// Work split: one workgroup = 128 queries of one (sequence, head); 8 waves.
+// Wave w owns query group w&3 (32 queries) and key half w>>2 (32 keys) of every
+// 64-key tile, keeping its own running max / sum / output; the two halves of a
+// query group are merged at the end. Scores are computed transposed
+// (S^T = K . Qu^T), so a lane's accumulator column is one query: the softmax
+// max/sum need one cross-lane exchange (lane ^ 32), and the exp'd scores are
+// already laid out as the B operand of the P.V MFMA (keys permuted
+// consistently with the V^T fragment). The position term is a band product
+// relK[jband] . Qv^T over the 64 relative positions a wave's 32 queries x 32
+// keys touch (2x the in-band work), written to a per-wave LDS scratch and read
+// back along the diagonal j = k + 31 - q_local — that read is the rel-shift.
+// The relK band lives in LDS as a ring of six 32-row blocks, so each key tile
+// fetches only its 64 new band rows; the next tile's K, V^T and new band rows
+// are fetched into registers while the current tile computes.
 //
 // Inputs are f16: K, V and relK exactly as the reference rounds them
 // (src/cpu/ops.rs:258-259, src/cpu/layer.rs:234-247); q+u and q+v rounded to
@@ -31,23 +37,37 @@ namespace {
 
 constexpr int BQ = 128;
 constexpr int BKV = 64;
-constexpr int KLD = HDIM + 8;  // halves per LDS row of K and relK
-constexpr int VLD = BKV + 8;   // halves per LDS row of V^T
-constexpr int BAND = BQ + BKV; // relK rows staged per key tile (191 used)
-constexpr int PLD = 100;       // floats per row of the band scratch (96 used)
+constexpr int KLD = HDIM + 8;   // halves per LDS row of K and relK
+constexpr int VLD = BKV + 8;    // halves per LDS row of V^T
+constexpr int BAND = BQ + BKV;  // relK rows staged per key tile (191 used)
+constexpr int PLD = 68;         // floats per row of a wave's band scratch (64 used)
+constexpr int NT = 512;         // threads per workgroup
 
-__global__ void __launch_bounds__(256) rel_attn_kernel(AttnArgs a, float scale_log2) {
-  __shared__ __attribute__((aligned(16))) half K_s[BKV * KLD];
-  __shared__ __attribute__((aligned(16))) half V_s[HDIM * VLD];
-  __shared__ __attribute__((aligned(16))) half R_s[BAND * KLD];
-  __shared__ __attribute__((aligned(16))) float P_s[4][32 * PLD];
+constexpr int K_CH = BKV * HDIM / 8 / NT;   // 16-byte chunks per thread
+constexpr int V_CH = HDIM * BKV / 8 / NT;
+constexpr int R_CH = BAND * HDIM / 8 / NT;
 
-  const int4 tile = a.tiles[blockIdx.x];
+struct Smem {
+  half K[BKV * KLD];
+  half V[HDIM * VLD];
+  half R[BAND * KLD];
+  float P[8][32 * PLD];
+};
+
+__global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem_raw[];
+  Smem& sm = *reinterpret_cast<Smem*>(smem_raw);
+
+  // Workgroups are dispatched round-robin over the 8 XCDs, so block b runs on
+  // XCD b % 8: giving head b % 8 to it keeps every query tile of one head on one
+  // XCD, whose L2 then holds that head's K, V^T and relK (2.2 MB at T = 2207).
+  const int h = blockIdx.x % HEADS;
+  const int4 tile = a.tiles[blockIdx.x / HEADS];
   const int start = tile.x, T = tile.y, q0 = tile.z;
-  const int h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int qg = wid & 3, kh = wid >> 2;
   const int l32 = lane & 31, lhi = lane >> 5;
-  const int q_lane = q0 + 32 * wid + l32;
+  const int q_lane = q0 + 32 * qg + l32;
   const int prows = 2 * a.tc - 1;
 
   // B-operand fragments of Qu^T / Qv^T: lane holds q_lane, dims 16s+8*lhi..+7.
@@ -76,67 +96,123 @@ __global__ void __launch_bounds__(256) rel_attn_kernel(AttnArgs a, float scale_l
   const half* kbase = a.kh + ((size_t)h * a.mp + start) * HDIM;
   const half* vbase = a.vt + (size_t)h * HDIM * a.mp + start;
   const half* rbase = a.rk + (size_t)h * a.pp * HDIM;
-  float* ps = P_s[wid];
+  float* ps = sm.P[wid];
   const uint4 zero4 = {0u, 0u, 0u, 0u};
 
-  for (int k0 = 0; k0 < T; k0 += BKV) {
-    // ---- stage K (64 x 128), V^T (128 x 64) and the relK band (192 x 128)
+  // Per-thread chunk coordinates (loop invariant). K and the relK rows: 16
+  // chunks of 8 halves per row; V^T: 8 chunks of 8 keys per d-row.
+  int k_row[K_CH], v_d[V_CH], v_kc[V_CH], r_row[2];
+  const int col16 = (tid & 15) * 8;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ch = tid + 256 * i, row = ch >> 4, col = (ch & 15) * 8;
-      uint4 v = zero4;
-      if (k0 + row < T) v = *reinterpret_cast<const uint4*>(kbase + (size_t)(k0 + row) * HDIM + col);
-      *reinterpret_cast<uint4*>(&K_s[row * KLD + col]) = v;
-    }
+  for (int i = 0; i < K_CH; ++i) k_row[i] = (tid + NT * i) >> 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ch = tid + 256 * i, d = ch >> 3, kc = (ch & 7) * 8;
-      uint4 v = zero4;
-      if (k0 + kc < T) {
-        v = *reinterpret_cast<const uint4*>(vbase + (size_t)d * a.mp + k0 + kc);
-        if (k0 + kc + 8 > T) {  // zero the keys past the sequence end
-          half8 hv = *reinterpret_cast<half8*>(&v);
+  for (int i = 0; i < V_CH; ++i) {
+    v_d[i] = (tid + NT * i) >> 3;
+    v_kc[i] = ((tid + NT * i) & 7) * 8;
+  }
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            if (k0 + kc + e >= T) hv[e] = (half)0.0f;
-          v = *reinterpret_cast<uint4*>(&hv);
-        }
-      }
-      *reinterpret_cast<uint4*>(&V_s[d * VLD + kc]) = v;
-    }
-    const int jg0 = a.tc - 1 - (q0 + BQ - 1) + k0;
-#pragma unroll
-    for (int i = 0; i < 12; ++i) {
-      const int ch = tid + 256 * i, row = ch >> 4, col = (ch & 15) * 8;
-      const int j = jg0 + row;
-      uint4 v = zero4;
-      if (j >= 0 && j < prows) v = *reinterpret_cast<const uint4*>(rbase + (size_t)j * HDIM + col);
-      *reinterpret_cast<uint4*>(&R_s[row * KLD + col]) = v;
-    }
-    __syncthreads();
+  for (int i = 0; i < 2; ++i) r_row[i] = (tid + NT * i) >> 4;
 
-    // ---- content scores S^T (64 keys x 32 queries)
-    floatx16 s[2];
+  // relK band as a ring of 6 blocks of 32 rows: band row r of key tile t lives
+  // in block ((r >> 5) + 2t) % 6. Each tile only fetches its last 64 rows
+  // (the first 128 are the previous tile's last 128).
+  const int jg00 = a.tc - 1 - (q0 + BQ - 1);  // band origin of tile 0
+  auto r_ok = [&](int j) { return j >= 0 && j < prows; };
+  for (int i = 0; i < R_CH; ++i) {  // tile 0: all 192 rows
+    const int ch = tid + NT * i, row = ch >> 4;
+    const int j = jg00 + row;
+    const uint4 v = r_ok(j) ? *reinterpret_cast<const uint4*>(rbase + (size_t)j * HDIM + col16) : zero4;
+    *reinterpret_cast<uint4*>(&sm.R[row * KLD + col16]) = v;
+  }
+
+  uint4 kr[K_CH], vr[V_CH], rr[2];
+  auto fetch = [&](int k0, int t) {
+    const bool interior = k0 + BKV <= T;
+    if (interior) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+      for (int i = 0; i < K_CH; ++i)
+        kr[i] = *reinterpret_cast<const uint4*>(kbase + (size_t)(k0 + k_row[i]) * HDIM + col16);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) s[kb][v] = 0.0f;
+      for (int i = 0; i < V_CH; ++i)
+        vr[i] = *reinterpret_cast<const uint4*>(vbase + (size_t)v_d[i] * a.mp + k0 + v_kc[i]);
+    } else {
 #pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        const half8 kf = ld_half8(&K_s[(kb * 32 + l32) * KLD + 16 * st + 8 * lhi]);
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, quf[st], s[kb], 0, 0, 0);
+      for (int i = 0; i < K_CH; ++i)
+        kr[i] = (k0 + k_row[i] < T)
+                    ? *reinterpret_cast<const uint4*>(kbase + (size_t)(k0 + k_row[i]) * HDIM + col16)
+                    : zero4;
+#pragma unroll
+      for (int i = 0; i < V_CH; ++i) {
+        uint4 v = zero4;
+        const int kc = v_kc[i];
+        if (k0 + kc < T) {
+          v = *reinterpret_cast<const uint4*>(vbase + (size_t)v_d[i] * a.mp + k0 + kc);
+          if (k0 + kc + 8 > T) {  // zero the keys past the sequence end
+            half8 hv = *reinterpret_cast<half8*>(&v);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (k0 + kc + e >= T) hv[e] = (half)0.0f;
+            v = *reinterpret_cast<uint4*>(&hv);
+          }
+        }
+        vr[i] = v;
       }
     }
-    // ---- position band relK[j] . Qv^T over this wave's 96 band rows
-    const int rb0 = 96 - 32 * wid;
+    const int jn = jg00 + 64 * t + 128;  // first new band row of tile t
+    if (jn >= 0 && jn + 64 <= prows) {
 #pragma unroll
-    for (int bb = 0; bb < 3; ++bb) {
+      for (int i = 0; i < 2; ++i)
+        rr[i] = *reinterpret_cast<const uint4*>(rbase + (size_t)(jn + r_row[i]) * HDIM + col16);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int j = jn + r_row[i];
+        rr[i] = r_ok(j) ? *reinterpret_cast<const uint4*>(rbase + (size_t)j * HDIM + col16) : zero4;
+      }
+    }
+  };
+  auto stage = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < K_CH; ++i) *reinterpret_cast<uint4*>(&sm.K[k_row[i] * KLD + col16]) = kr[i];
+#pragma unroll
+    for (int i = 0; i < V_CH; ++i) *reinterpret_cast<uint4*>(&sm.V[v_d[i] * VLD + v_kc[i]]) = vr[i];
+    if (t > 0) {  // new band rows 128..191 of tile t -> ring blocks (4,5) + 2t
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r = 128 + r_row[i];
+        const int prow = (((r >> 5) + 2 * t) % 6) * 32 + (r & 31);
+        *reinterpret_cast<uint4*>(&sm.R[prow * KLD + col16]) = rr[i];
+      }
+    }
+  };
+
+  const int rb0 = 96 - 32 * qg + 32 * kh;  // first band row of this wave
+  fetch(0, 0);
+  int t = 0;
+  for (int k0 = 0; k0 < T; k0 += BKV, ++t) {
+    stage(t);
+    __syncthreads();
+    if (k0 + BKV < T) fetch(k0 + BKV, t + 1);
+
+    // ---- content scores S^T (this wave's 32 keys x 32 queries)
+    floatx16 s;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s[v] = 0.0f;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const half8 kf = ld_half8(&sm.K[(32 * kh + l32) * KLD + 16 * st + 8 * lhi]);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, quf[st], s, 0, 0, 0);
+    }
+    // ---- position band relK[j] . Qv^T over the wave's 64 band rows
+#pragma unroll
+    for (int bb = 0; bb < 2; ++bb) {
       floatx16 bd;
 #pragma unroll
       for (int v = 0; v < 16; ++v) bd[v] = 0.0f;
+      const int pblk = ((rb0 >> 5) + bb + 2 * t) % 6;  // ring block of band rows rb0+32bb..
 #pragma unroll
       for (int st = 0; st < 8; ++st) {
-        const half8 rf = ld_half8(&R_s[(rb0 + bb * 32 + l32) * KLD + 16 * st + 8 * lhi]);
+        const half8 rf = ld_half8(&sm.R[(pblk * 32 + l32) * KLD + 16 * st + 8 * lhi]);
         bd = __builtin_amdgcn_mfma_f32_32x32x16_f16(rf, qvf[st], bd, 0, 0, 0);
       }
 #pragma unroll
@@ -145,50 +221,52 @@ __global__ void __launch_bounds__(256) rel_attn_kernel(AttnArgs a, float scale_l
         *reinterpret_cast<floatx4*>(&ps[l32 * PLD + 32 * bb + 8 * g + 4 * lhi]) = w4;
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- rel-shift + scale + mask, online softmax
+    // ---- rel-shift (diagonal read), mask, online softmax (log2 domain)
+    const bool tail = k0 + BKV > T;
     float mt = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int kk = 32 * kb + 8 * (v >> 2) + 4 * lhi + (v & 3);
-        float x = (s[kb][v] + ps[l32 * PLD + kk + 31 - l32]) * scale_log2;
-        if (k0 + kk >= T) x = -INFINITY;
-        s[kb][v] = x;
-        mt = fmaxf(mt, x);
-      }
+    for (int v = 0; v < 16; ++v) {
+      const int kk = 8 * (v >> 2) + 4 * lhi + (v & 3);  // key within the wave's half
+      float x = s[v] + ps[l32 * PLD + kk + 31 - l32];
+      if (tail && k0 + 32 * kh + kk >= T) x = -INFINITY;
+      s[v] = x;
+      mt = fmaxf(mt, x);
+    }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float m_new = fmaxf(m_run, mt);
-    const float corr = exp2f(m_run - m_new);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // a half with no valid key yet
     float ls = 0.0f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float pv = exp2f(s[kb][v] - m_new);
-        s[kb][v] = pv;
-        ls += pv;
-      }
+    for (int v = 0; v < 16; ++v) {
+      const float pv = __builtin_amdgcn_exp2f(s[v] - m_use);
+      s[v] = pv;
+      ls += pv;
+    }
     ls += __shfl_xor(ls, 32, 64);
-    l_run = l_run * corr + ls;
+    if (__any(m_new > m_run)) {  // rescale only when some running max moved
+      const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
+      l_run *= corr;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[db][v] *= corr;
+    }
+    l_run += ls;
     m_run = m_new;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[db][v] *= corr;
 
-    // ---- O^T (128 d x 32 q) += V^T . P^T over 4 steps of 16 keys
+    // ---- O^T (128 d x 32 q) += V^T . P^T over this wave's 32 keys
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const int kb = st >> 1, vb = 8 * (st & 1);
+    for (int st = 0; st < 2; ++st) {
       half8 pf;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pf[e] = (half)s[kb][vb + e];
+      for (int e = 0; e < 8; ++e) pf[e] = (half)s[8 * st + e];
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const half* vp = &V_s[(32 * db + l32) * VLD + 16 * st + 4 * lhi];
+        const half* vp = &sm.V[(32 * db + l32) * VLD + 32 * kh + 16 * st + 4 * lhi];
         const half4 lo = *reinterpret_cast<const half4*>(vp);
         const half4 hi = *reinterpret_cast<const half4*>(vp + 8);
         const half8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -198,15 +276,35 @@ __global__ void __launch_bounds__(256) rel_attn_kernel(AttnArgs a, float scale_l
     __syncthreads();
   }
 
-  if (q_lane < T) {
-    const float inv = 1.0f / l_run;
+  // ---- merge the two key halves of each query group (through LDS), write out
+  float* xo = reinterpret_cast<float*>(sm.K);  // reuses the K/V/relK staging area
+  float* xm = xo + 4 * 64 * 64;
+  if (kh == 1) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) xo[(qg * 64 + db * 16 + v) * 64 + lane] = o[db][v];
+    xm[(qg * 2) * 64 + lane] = m_run;
+    xm[(qg * 2 + 1) * 64 + lane] = l_run;
+  }
+  __syncthreads();
+  if (kh == 0 && q_lane < T) {
+    const float m1 = xm[(qg * 2) * 64 + lane], l1 = xm[(qg * 2 + 1) * 64 + lane];
+    const float m = fmaxf(m_run, m1);
+    const float c0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+    const float c1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
+    const float inv = 1.0f / (l_run * c0 + l1 * c1);
     half* orow = a.out + (size_t)(start + q_lane) * HIDDEN + h * HDIM;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const half4 w4 = {(half)(o[db][4 * g] * inv), (half)(o[db][4 * g + 1] * inv),
-                          (half)(o[db][4 * g + 2] * inv), (half)(o[db][4 * g + 3] * inv)};
+        half4 w4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int v = 4 * g + i;
+          w4[i] = (half)((o[db][v] * c0 + xo[(qg * 64 + db * 16 + v) * 64 + lane] * c1) * inv);
+        }
         *reinterpret_cast<half4*>(orow + 32 * db + 8 * g + 4 * lhi) = w4;
       }
   }
@@ -217,10 +315,19 @@ __global__ void __launch_bounds__(256) rel_attn_kernel(AttnArgs a, float scale_l
 void rel_attention(const AttnArgs& a, hipStream_t stream) {
   BARK_REQUIRE(a.ntiles > 0 && a.tiles, "rel_attention: no query tiles");
   BARK_REQUIRE(a.mp % 64 == 0 && a.pp >= 2 * a.tc - 1, "rel_attention: bad buffer shape");
-  const float scale_log2 = (1.0f / sqrtf((float)HDIM)) * 1.4426950408889634f;
-  hipLaunchKernelGGL(rel_attn_kernel, dim3(a.ntiles, HEADS), dim3(256), 0, stream, a,
-                     scale_log2);
+  static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget");
+  static_assert(4 * 64 * 64 * 4 + 8 * 64 * 4 <= BKV * KLD * 2 + HDIM * VLD * 2 + BAND * KLD * 2,
+                "merge area must fit in the staging area");
+  static bool attr = [] {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(rel_attn_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(Smem)) == hipSuccess;
+  }();
+  BARK_REQUIRE(attr, "rel_attention: cannot reserve LDS");
+  hipLaunchKernelGGL(rel_attn_kernel, dim3(a.ntiles * HEADS), dim3(NT), sizeof(Smem), stream, a);
   BARK_HIP_CHECK(hipGetLastError());
 }
+
+// scale * log2(e) applied to q+u and q+v by the qkv epilogue
+float attention_q_scale() { return (1.0f / sqrtf((float)HDIM)) * 1.4426950408889634f; }
 
 }  // namespace bark

@@ -625,6 +625,7 @@ struct BarkHip {
       e.bu = L.bu;
       e.bv = L.bv;
       e.mp = mp;
+      e.scale = attention_q_scale();
       gemm_op("qkv_heads", xnp, HIDDEN, mp, mr, L.qkv, Epi::Qkv, e, 2.0 * 4096, st);
       e = EpiArgs();
       e.rk = rk.as<half>();

@@ -126,8 +126,8 @@ __device__ inline void store_one(const EpiArgs& ea, int r, int c, float v) {
     const int which = c >> 10, hd = c & 1023, h = hd >> 7, d = hd & 127;
     const size_t hr = ((size_t)h * ea.mp + r) * HDIM + d;
     if (which == 0) {
-      ea.qu[hr] = (half)(v + ea.bu[hd]);
-      ea.qv[hr] = (half)(v + ea.bv[hd]);
+      ea.qu[hr] = (half)((v + ea.bu[hd]) * ea.scale);
+      ea.qv[hr] = (half)((v + ea.bv[hd]) * ea.scale);
     } else if (which == 1) {
       ea.kh[hr] = (half)v;
     } else {

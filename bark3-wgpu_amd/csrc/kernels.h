@@ -17,7 +17,7 @@ enum class Epi : int {
   Silu = 2,          // out_f16[r][c] = f16(silu(v))
   Resid = 3,         // out_f32[r][c] += scale * v
   Glu = 4,           // out_f32[r][c/2 pair] = a * sigmoid(b) (rows of W interleaved)
-  Qkv = 5,           // head packing of q+bias_u, q+bias_v, k, v^T (f16)
+  Qkv = 5,           // head packing of scale*(q+bias_u), scale*(q+bias_v), k, v^T (f16)
   RelK = 6,          // rk[h][r][d] = f16(v)
   BiasReluF16 = 7,   // out_f16[r][c] = f16(max(v + bias[c], 0))
   FlattenReluF16 = 8, // pixel r = (t, m): out_f16[t][c*16+m] = f16(max(v+bias[c],0))
@@ -71,7 +71,10 @@ struct AttnArgs {
   const int4* tiles;
   int ntiles;
 };
+// q+u and q+v must be pre-multiplied by attention_q_scale() = log2(e)/sqrt(128)
+// (the Qkv epilogue does it when EpiArgs::scale is set to this value).
 void rel_attention(const AttnArgs& a, hipStream_t stream);
+float attention_q_scale();
 
 // ----------------------------------------------------------------- ops --
 // LayerNorm over 1024 columns. y16 and/or y32 may be null.
