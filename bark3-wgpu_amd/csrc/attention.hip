@@ -194,32 +194,28 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
     __syncthreads();
     if (k0 + BKV < T) fetch(k0 + BKV, t + 1);
 
-    // ---- content scores S^T (this wave's 32 keys x 32 queries)
-    floatx16 s;
+    // ---- content scores S^T (this wave's 32 keys x 32 queries) and the
+    // position band relK[j] . Qv^T over the wave's 64 band rows: three
+    // independent MFMA chains, interleaved so they overlap in the pipeline
+    floatx16 s, bd0, bd1;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) s[v] = 0.0f;
+    for (int v = 0; v < 16; ++v) s[v] = bd0[v] = bd1[v] = 0.0f;
+    const int pb0 = ((rb0 >> 5) + 2 * t) % 6, pb1 = ((rb0 >> 5) + 1 + 2 * t) % 6;  // ring blocks
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
       const half8 kf = ld_half8(&sm.K[(32 * kh + l32) * KLD + 16 * st + 8 * lhi]);
+      const half8 r0 = ld_half8(&sm.R[(pb0 * 32 + l32) * KLD + 16 * st + 8 * lhi]);
+      const half8 r1 = ld_half8(&sm.R[(pb1 * 32 + l32) * KLD + 16 * st + 8 * lhi]);
       s = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, quf[st], s, 0, 0, 0);
+      bd0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(r0, qvf[st], bd0, 0, 0, 0);
+      bd1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(r1, qvf[st], bd1, 0, 0, 0);
     }
-    // ---- position band relK[j] . Qv^T over the wave's 64 band rows
 #pragma unroll
-    for (int bb = 0; bb < 2; ++bb) {
-      floatx16 bd;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) bd[v] = 0.0f;
-      const int pblk = ((rb0 >> 5) + bb + 2 * t) % 6;  // ring block of band rows rb0+32bb..
-#pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        const half8 rf = ld_half8(&sm.R[(pblk * 32 + l32) * KLD + 16 * st + 8 * lhi]);
-        bd = __builtin_amdgcn_mfma_f32_32x32x16_f16(rf, qvf[st], bd, 0, 0, 0);
-      }
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        floatx4 w4 = {bd[4 * g], bd[4 * g + 1], bd[4 * g + 2], bd[4 * g + 3]};
-        *reinterpret_cast<floatx4*>(&ps[l32 * PLD + 32 * bb + 8 * g + 4 * lhi]) = w4;
-      }
+    for (int g = 0; g < 4; ++g) {
+      const floatx4 w0 = {bd0[4 * g], bd0[4 * g + 1], bd0[4 * g + 2], bd0[4 * g + 3]};
+      const floatx4 w1 = {bd1[4 * g], bd1[4 * g + 1], bd1[4 * g + 2], bd1[4 * g + 3]};
+      *reinterpret_cast<floatx4*>(&ps[l32 * PLD + 8 * g + 4 * lhi]) = w0;
+      *reinterpret_cast<floatx4*>(&ps[l32 * PLD + 32 + 8 * g + 4 * lhi]) = w1;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -237,8 +233,21 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
       mt = fmaxf(mt, x);
     }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m_run, mt);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // a half with no valid key yet
+    // Lazy rescaling: exp2 is taken against a reference max m_run that is only
+    // raised when a new score exceeds it by more than 8 (log2 units), so
+    // p <= 256 and the output/sum rescale runs rarely. Softmax is invariant to
+    // the reference, so this is exact up to rounding.
+    if (__any(mt > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float corr = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= corr;
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[db][v] *= corr;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;  // a half with no valid key yet
     float ls = 0.0f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -247,16 +256,7 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
       ls += pv;
     }
     ls += __shfl_xor(ls, 32, 64);
-    if (__any(m_new > m_run)) {  // rescale only when some running max moved
-      const float corr = __builtin_amdgcn_exp2f(m_run - m_use);
-      l_run *= corr;
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[db][v] *= corr;
-    }
     l_run += ls;
-    m_run = m_new;
 
     // ---- O^T (128 d x 32 q) += V^T . P^T over this wave's 32 keys
 #pragma unroll
