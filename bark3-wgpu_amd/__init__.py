@@ -140,6 +140,7 @@ _SIGS = {
         ],
     ),
     "bark_hip_profile": (_c.c_int, [_c.c_void_p, _c.c_int]),
+    "bark_hip_profile_only": (_c.c_int, [_c.c_void_p, _c.c_char_p]),
     "bark_hip_profile_report": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_size_t]),
     "bark_hip_lowbit_linear": (
         _c.c_int,
@@ -315,6 +316,10 @@ class HipEncoder:
     def profile(self, enable: bool = True) -> None:
         """Per-operator HIP-event timing of the forward (BARK3_ENC_PROFILE)."""
         _check(lib().bark_hip_profile(self._h, 1 if enable else 0))
+
+    def profile_only(self, label: str | None) -> None:
+        """Time only the launches labelled `label` (None = all)."""
+        _check(lib().bark_hip_profile_only(self._h, label.encode() if label else None))
 
     def profile_report(self) -> dict:
         """{label: {count, ms, flops, bytes}} since the last report."""

@@ -73,7 +73,7 @@ struct HostLinear {
 };
 
 struct DevLayer {
-  GemmWeight qkv, relk, o, ff1a, ff1b, ff2a, ff2b, pw1, pw2;
+  GemmWeight qkv, o, ff1a, ff1b, ff2a, ff2b, pw1, pw2;
   float *dw = nullptr, *bn_a = nullptr, *bn_b = nullptr, *bu = nullptr, *bv = nullptr;
   float* ln_w[5] = {};
   float* ln_b[5] = {};
@@ -100,6 +100,7 @@ struct Profiler {
     hipEvent_t a, b;
   };
   bool on = false;
+  std::string only;  // non-empty: time this label only
   std::vector<hipEvent_t> free_events;
   std::vector<Op> ops;
 
@@ -115,7 +116,7 @@ struct Profiler {
   }
   template <class F>
   void run(const char* label, double flops, double bytes, hipStream_t st, F&& f) {
-    if (!on) {
+    if (!on || (!only.empty() && only != label)) {
       f();
       return;
     }
@@ -189,6 +190,9 @@ struct BarkHip {
   Profiler prof;
   std::vector<int> table_key;  // plan whose row bounds / query tiles are on the device
   GemmWeight sub_w, proj_w, sub_pw1, sub_pw2;
+  // relative_k_proj of every layer stacked (row block l = layer l): the
+  // position keys depend on T only, so all layers' relK come from one GEMM.
+  GemmWeight relk_all;
   float *sub_b = nullptr, *proj_b = nullptr;
   float *l0w = nullptr, *l0b = nullptr, *l2w = nullptr, *l2b = nullptr, *l3b = nullptr;
   float *l5w = nullptr, *l5b = nullptr, *l6b = nullptr;
@@ -351,6 +355,7 @@ struct BarkHip {
     proj_w = to_device(linear("encoder_projector.weight", PROJ, HIDDEN, false));
     proj_b = f32_dev("encoder_projector.bias", PROJ);
     layers.resize(n_layers);
+    std::vector<HostLinear> relk;
     for (int l = 0; l < n_layers; ++l) {
       const std::string p = "encoder.layers." + std::to_string(l) + ".";
       DevLayer& L = layers[l];
@@ -358,7 +363,7 @@ struct BarkHip {
                                linear(p + "self_attn.k_proj.weight", 1024, 1024, true),
                                linear(p + "self_attn.v_proj.weight", 1024, 1024, true)},
                               "fused q/k/v"));
-      L.relk = to_device(linear(p + "self_attn.relative_k_proj.weight", 1024, 1024, true));
+      relk.push_back(linear(p + "self_attn.relative_k_proj.weight", 1024, 1024, true));
       L.o = to_device(linear(p + "self_attn.o_proj.weight", 1024, 1024, true));
       L.ff1a = to_device(linear(p + "feed_forward1.linear1.weight", 4096, 1024, true));
       L.ff1b = to_device(linear(p + "feed_forward1.linear2.weight", 1024, 4096, true));
@@ -392,6 +397,7 @@ struct BarkHip {
       L.bu = f32_dev(p + "self_attn.bias_u", 1024);
       L.bv = f32_dev(p + "self_attn.bias_v", 1024);
     }
+    relk_all = to_device(stack(relk, "relative_k_proj"));
     // conv front end (optional: encode_sub does not need it)
     const std::string s = "encoder.subsampling.layers.";
     has_front_end = staged.count(s + "0.weight") > 0;
@@ -484,7 +490,7 @@ struct BarkHip {
     ensure(qv, HEADS * mp * HDIM * 2);
     ensure(kh, HEADS * mp * HDIM * 2);
     ensure(vt, HEADS * mp * HDIM * 2);
-    ensure(rk, HEADS * pp * HDIM * 2);
+    ensure(rk, (size_t)n_layers * HEADS * pp * HDIM * 2);
     ensure(ao, mp * HIDDEN * 2);
     ensure(h, mp * HIDDEN * 4);
     ensure(h2, mp * HIDDEN * 4);
@@ -600,6 +606,12 @@ struct BarkHip {
     gemm_op("sub_linear", sub16.as<half>(), 4096, mp, mr, sub_w, Epi::StoreF32, es, 4.0 * HIDDEN, st);
 
     const half* pos_rows = pos.as<half>() + (size_t)(pos_t - tc) * HIDDEN;
+    {  // position keys of all layers: rk[l][h][r][d]
+      EpiArgs e;
+      e.rk = rk.as<half>();
+      e.pp = pp;
+      gemm_op("relk", pos_rows, HIDDEN, prows, prows, relk_all, Epi::RelK, e, 2.0 * HIDDEN * n_layers, st);
+    }
     for (int l = 0; l < n_layers; ++l) {
       const DevLayer& L = layers[l];
       if (l == 0)
@@ -627,11 +639,8 @@ struct BarkHip {
       e.mp = mp;
       e.scale = attention_q_scale();
       gemm_op("qkv_heads", xnp, HIDDEN, mp, mr, L.qkv, Epi::Qkv, e, 2.0 * 4096, st);
-      e = EpiArgs();
-      e.rk = rk.as<half>();
-      e.pp = pp;
-      gemm_op("relk", pos_rows, HIDDEN, prows, prows, L.relk, Epi::RelK, e, 2.0 * HIDDEN, st);
-      AttnArgs aa{qu.as<half>(), qv.as<half>(), kh.as<half>(), vt.as<half>(), rk.as<half>(),
+      AttnArgs aa{qu.as<half>(), qv.as<half>(), kh.as<half>(), vt.as<half>(),
+                  rk.as<half>() + (size_t)l * HEADS * pp * HDIM,
                   ao.as<half>(), mp, pp, tc, tiles.as<int4>(), ntiles};
       prof.run("rel_attention", attn_flops, 2.0 * mr * HIDDEN * 5 + 2.0 * prows * HIDDEN, st,
                [&] { rel_attention(aa, st); });
@@ -963,6 +972,16 @@ int bark_hip_profile(BarkHip* h, int enable) {
     BARK_HIP_CHECK(hipSetDevice(h->device));
     (void)h->prof.report();  // drop anything recorded so far
     h->prof.on = enable != 0;
+  });
+}
+
+int bark_hip_profile_only(BarkHip* h, const char* label) {
+  return guarded([&] {
+    BARK_REQUIRE(h, "null handle");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    (void)h->prof.report();
+    h->prof.only = label ? label : "";
   });
 }
 

@@ -376,6 +376,242 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
   }
 }
 
+// Wide-tile kernel: workgroup tile (32*FM) x 256, the four waves side by
+// side, each owning all rows and 64 columns (FM x 2 MFMA blocks). B never
+// touches LDS: an MFMA B fragment is 8 consecutive k of one weight row, i.e.
+// one u32 of 4-bit codes (expanded in registers with the lane's two row
+// tables) or 16 bytes of f16 weights. Only A is staged through LDS. The k
+// order inside each 64-k tile is permuted identically on both operands (lane
+// half h, slice s covers k = 32h + 8s .. +7), so a lane's B data for a whole
+// k-tile is contiguous: one 16-byte load of codes or four of f16. Both weight
+// formats therefore accumulate in the same order and give bit-identical
+// results for the same weight values. Per k-tile a wave runs 8*FM MFMAs
+// against 4*FM fragment reads (and 8 code expansions in 4-bit mode).
+template <int FM, bool LUT4, bool SWZ, bool ABF16, int EPI>
+__global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
+  constexpr int BM = 32 * FM;
+  constexpr int A_CH = BM * BK / 8 / 256;  // 16-byte chunks of A per thread per k-tile (= FM)
+  constexpr int B_V = LUT4 ? 2 : 8;        // 16-byte loads of B per lane per k-tile
+  constexpr int BD = LUT4 ? 4 : 2;         // k-tiles of B in flight (register stages)
+  __shared__ __attribute__((aligned(16))) half As[2][BM * LDK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const int n0 = blockIdx.x * 256, m0 = blockIdx.y * BM;
+  const int nw = n0 + wid * 64;
+
+  RowLut lut[2];
+  const uint8_t* brow[2];  // this lane's B bytes of k-tile 0, for its two rows
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = nw + 32 * j + l32;
+    if constexpr (LUT4) {
+      lut[j] = load_row_lut(p.lut + (size_t)n * 16);
+      brow[j] = p.codes + (size_t)n * (p.K >> 1) + 16 * lhi;
+    } else {
+      brow[j] = reinterpret_cast<const uint8_t*>(p.W + (size_t)n * p.K + 32 * lhi);
+    }
+  }
+  constexpr int B_TILE_BYTES = LUT4 ? BK / 2 : BK * 2;
+  const half* arow[A_CH];
+  int a_lds[A_CH];
+#pragma unroll
+  for (int i = 0; i < A_CH; ++i) {
+    const int ch = tid + 256 * i, row = ch >> 3, col = (ch & 7) * 8;
+    arow[i] = p.A + (size_t)min(m0 + row, p.M - 1) * p.lda + col;  // rows past M repeat row M-1
+    a_lds[i] = row * LDK + col;
+  }
+
+  struct AStage {
+    uint4 v[A_CH];
+  };
+  struct BStage {
+    uint4 v[B_V];
+  };
+  AStage ra0, ra1, ra2, ra3;
+  BStage rb0, rb1, rb2, rb3;  // f16 mode uses rb0/rb1 only
+
+  // Loads past the last k-tile re-read it (no branch, stays in bounds).
+  const int nk = p.K / BK;
+  auto load_a = [&](int kt, AStage& a) {
+    kt = min(kt, nk - 1);
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) a.v[i] = *reinterpret_cast<const uint4*>(arow[i] + kt * BK);
+  };
+  auto load_b = [&](int kt, BStage& b) {
+    kt = min(kt, nk - 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < B_V / 2; ++q)
+        b.v[j * (B_V / 2) + q] = *reinterpret_cast<const uint4*>(brow[j] + (size_t)kt * B_TILE_BYTES + 16 * q);
+  };
+  auto store_chunk = [&](int buf, const AStage& a, int i) {
+    if constexpr (ABF16) {
+      const uint32_t w4[4] = {a.v[i].x, a.v[i].y, a.v[i].z, a.v[i].w};
+      half8 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[2 * e] = (half)__uint_as_float(w4[e] << 16);
+        v[2 * e + 1] = (half)__uint_as_float(w4[e] & 0xffff0000u);
+      }
+      st_half8(&As[buf][a_lds[i]], v);
+    } else {
+      const uint4 t{a.v[i].x, a.v[i].y, a.v[i].z, a.v[i].w};
+      *reinterpret_cast<uint4*>(&As[buf][a_lds[i]]) = t;
+    }
+  };
+
+  floatx16 acc[FM][2];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // A fragment row offset of block i for this lane, k slice s: chunk 4*lhi + s.
+  const int af_off = l32 * LDK + 32 * lhi;
+  auto read_af = [&](half8 (&af)[FM], int buf, int s) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[i] = ld_half8(&As[buf][af_off + i * 32 * LDK + 8 * s]);
+  };
+  auto code_word = [](const uint4& c, int s) { return s == 0 ? c.x : s == 1 ? c.y : s == 2 ? c.z : c.w; };
+  auto b_frag = [&](const BStage& b, int j, int s) {
+    uint4 q;
+    if constexpr (LUT4) {
+      q = expand8<SWZ>(code_word(b.v[j], s), lut[j]);
+    } else {
+      q = uint4{b.v[4 * j + s].x, b.v[4 * j + s].y, b.v[4 * j + s].z, b.v[4 * j + s].w};
+    }
+    return *reinterpret_cast<const half8*>(&q);
+  };
+
+  // One k-tile from LDS buffer `cur` and B stage `bs`; meanwhile stores the
+  // next tile's A (register stage `as`) into buffer `nxt`.
+  auto tile = [&](int cur, int nxt, const BStage& bs, const AStage& as) {
+    half8 af[2][FM];
+    half8 bf[2][2];
+    read_af(af[0], cur, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) bf[0][j] = b_frag(bs, j, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = s & 1, n = c ^ 1;
+      if (s < 3) {
+        read_af(af[n], cur, s + 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) bf[n][j] = b_frag(bs, j, s + 1);
+      }
+#pragma unroll
+      for (int i = 0; i < A_CH; ++i)
+        if (i * 4 / A_CH == s) store_chunk(nxt, as, i);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
+      if (s < 3) {
+        constexpr int VPER = LUT4 ? (52 + 2 * FM - 1) / (2 * FM) : 1;
+        __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
+#pragma unroll
+        for (int m = 0; m < 2 * FM; ++m) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, VPER, 0);
+        }
+      }
+    }
+  };
+
+  // Per k-tile kt: LDS buffer kt%2 holds A(kt); A(kt+1) is stored from its
+  // register stage during the tile; loads for A(kt+4) and B(kt+BD) refill the
+  // stages the tile freed. Past the end the stores repeat the last tile into
+  // a buffer that is never read again.
+  load_a(0, ra0);
+  load_b(0, rb0);
+  load_a(1, ra1);
+  load_b(1, rb1);
+  load_a(2, ra2);
+  if constexpr (LUT4) load_b(2, rb2);
+  load_a(3, ra3);
+  if constexpr (LUT4) load_b(3, rb3);
+#pragma unroll
+  for (int i = 0; i < A_CH; ++i) store_chunk(0, ra0, i);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 4) {
+    tile(0, 1, rb0, ra1);
+    load_a(kt + 4, ra0);
+    load_b(kt + BD, rb0);
+    __syncthreads();
+    tile(1, 0, rb1, ra2);
+    load_a(kt + 5, ra1);
+    load_b(kt + 1 + BD, rb1);
+    __syncthreads();
+    tile(0, 1, LUT4 ? rb2 : rb0, ra3);
+    load_a(kt + 6, ra2);
+    load_b(kt + 2 + BD, LUT4 ? rb2 : rb0);
+    __syncthreads();
+    tile(1, 0, LUT4 ? rb3 : rb1, ra0);
+    load_a(kt + 7, ra3);
+    load_b(kt + 3 + BD, LUT4 ? rb3 : rb1);
+    __syncthreads();
+  }
+
+  const EpiArgs& ea = p.ea;
+  if constexpr (EPI == (int)Epi::Glu) {
+    const int c = (nw >> 1) + l32;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = m0 + i * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
+        if (r >= p.M) continue;
+        ea.out_f32[(size_t)r * ea.ldo + c] = fast_sigmoid_mul(acc[i][0][v], acc[i][1][v]);
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = m0 + i * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
+          if (r < p.M) store_one<EPI>(ea, r, nw + 32 * j + l32, acc[i][j][v]);
+        }
+  }
+}
+
+// Weight format: 0 = f16, 1 = swizzled 4-bit (encoder), 2 = plain 4-bit
+// (isolated linear; f16 or bf16 activations).
+template <int FM>
+void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t s) {
+  dim3 grid(p.N / 256, ceil_div(p.M, 32 * FM)), block(256);
+#define BARK_K(L4, SW, AB, E) \
+  hipLaunchKernelGGL((gemm_wide_kernel<FM, L4, SW, AB, (int)Epi::E>), grid, block, 0, s, p)
+#define BARK_CASE(E)                                   \
+  case Epi::E:                                         \
+    if (fmt == 0) BARK_K(false, false, false, E);      \
+    else if (fmt == 1) BARK_K(true, true, false, E);   \
+    else if (abf16) BARK_K(true, false, true, E);      \
+    else BARK_K(true, false, false, E);                \
+    break;
+  switch (epi) {
+    BARK_CASE(StoreF32)
+    BARK_CASE(StoreF16)
+    BARK_CASE(StoreBF16)
+    BARK_CASE(Silu)
+    BARK_CASE(Resid)
+    BARK_CASE(ResidHalf)
+    BARK_CASE(Glu)
+    BARK_CASE(Qkv)
+    BARK_CASE(RelK)
+    BARK_CASE(BiasReluF16)
+    BARK_CASE(FlattenReluF16)
+  }
+#undef BARK_CASE
+#undef BARK_K
+}
+
 // Full epilogue set: f16 weights and swizzled 4-bit weights (the encoder).
 template <int BM, bool LUT4, bool SWZ>
 void launch_full(const GemmParams& p, Epi epi, hipStream_t s) {
@@ -435,6 +671,20 @@ int pick_bm(int M, int N) {
   return (tiles128 >= 256 && N < 4096) ? 128 : 64;
 }
 
+// 32-row MFMA blocks per wide tile (0 = use the 128-column kernel). Four
+// (128-row tiles) when that makes at least half a launch of one workgroup per
+// CU without a second, mostly idle round, two otherwise; from a sweep of the
+// encoder shapes on MI355X. BARK_HIP_GEMM_WIDE = 0/2/4 forces a choice.
+int pick_wide_fm(int M, int N) {
+  static const int forced = [] {
+    const char* e = getenv("BARK_HIP_GEMM_WIDE");
+    return e ? atoi(e) : -1;
+  }();
+  if (forced == 0 || forced == 2 || forced == 4) return forced;
+  const long tiles4 = (long)ceil_div(M, 128) * (N / 256);
+  return (tiles4 >= 128 && (tiles4 <= 256 || tiles4 >= 512)) ? 4 : 2;
+}
+
 }  // namespace
 
 void swizzle_codes(uint8_t* codes, size_t nbytes) {
@@ -458,8 +708,16 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   BARK_REQUIRE(lda >= W.k && lda % 8 == 0, "gemm: lda must be >= K and a multiple of 8");
   BARK_REQUIRE(W.lut4() ? (W.lut != nullptr) : (W.w16 != nullptr), "gemm: weight not set");
   GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea};
-  const int bm = pick_bm(M, W.n);
   BARK_REQUIRE(!a_bf16 || (W.lut4() && !W.swizzled), "gemm: bf16 activations need plain 4-bit weights");
+  const int fm = W.n % 256 == 0 ? pick_wide_fm(M, W.n) : 0;
+  if (fm) {
+    const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
+    if (fm == 4) launch_wide<4>(p, epi, fmt, a_bf16, stream);
+    else launch_wide<2>(p, epi, fmt, a_bf16, stream);
+    BARK_HIP_CHECK(hipGetLastError());
+    return;
+  }
+  const int bm = pick_bm(M, W.n);
 #define BARK_BM(BMV)                                             \
   if (bm == BMV) {                                               \
     if (!W.lut4()) launch_full<BMV, false, false>(p, epi, stream); \

@@ -111,6 +111,10 @@ int bark_hip_encode_mel_batch_device(BarkHip *h, const float *d_mel, const int32
  * launch of the forward is bracketed by HIP events on its stream. Enabling or
  * disabling discards what was recorded. */
 int bark_hip_profile(BarkHip *h, int enable);
+/* Restricts the per-operator timing to launches labelled `label` (NULL or ""
+ * = every launch), so a benchmark can time one kernel inside its timed region
+ * without bracketing all the others. Discards what was recorded. */
+int bark_hip_profile_only(BarkHip *h, const char *label);
 /* Writes JSON {label: {count, ms, flops, bytes}} aggregated over everything
  * recorded since the last report (flops/bytes are the algorithmic work of the
  * launches) and clears it. Synchronises with the recorded work. */
