@@ -393,6 +393,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   constexpr int A_CH = BM * BK / 8 / 256;  // 16-byte chunks of A per thread per k-tile (= FM)
   constexpr int B_V = LUT4 ? 2 : 8;        // 16-byte loads of B per lane per k-tile
   constexpr int BD = LUT4 ? 4 : 2;         // k-tiles of B in flight (register stages)
+  constexpr int AD = FM >= 8 ? 2 : 4;      // k-tiles of A in flight (register stages)
   __shared__ __attribute__((aligned(16))) half As[2][BM * LDK];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -400,25 +401,26 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   const int n0 = blockIdx.x * 256, m0 = blockIdx.y * BM;
   const int nw = n0 + wid * 64;
 
+  // Global addresses are a wave-uniform base plus 32-bit lane offsets (the
+  // host checks the operands fit), so loads use scalar base registers.
   RowLut lut[2];
-  const uint8_t* brow[2];  // this lane's B bytes of k-tile 0, for its two rows
+  const uint8_t* bbase = LUT4 ? p.codes : reinterpret_cast<const uint8_t*>(p.W);
+  constexpr int B_ROW_BYTES_PER_K2 = LUT4 ? 1 : 4;  // bytes per row per 2 k
+  uint32_t boff[2];  // this lane's B bytes of k-tile 0, for its two rows
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int n = nw + 32 * j + l32;
-    if constexpr (LUT4) {
-      lut[j] = load_row_lut(p.lut + (size_t)n * 16);
-      brow[j] = p.codes + (size_t)n * (p.K >> 1) + 16 * lhi;
-    } else {
-      brow[j] = reinterpret_cast<const uint8_t*>(p.W + (size_t)n * p.K + 32 * lhi);
-    }
+    if constexpr (LUT4) lut[j] = load_row_lut(p.lut + (size_t)n * 16);
+    boff[j] = (uint32_t)n * (uint32_t)(p.K / 2 * B_ROW_BYTES_PER_K2) + (LUT4 ? 16 : 64) * lhi;
   }
   constexpr int B_TILE_BYTES = LUT4 ? BK / 2 : BK * 2;
-  const half* arow[A_CH];
+  const half* abase = p.A + (size_t)m0 * p.lda;
+  uint32_t aoff[A_CH];
   int a_lds[A_CH];
 #pragma unroll
   for (int i = 0; i < A_CH; ++i) {
     const int ch = tid + 256 * i, row = ch >> 3, col = (ch & 7) * 8;
-    arow[i] = p.A + (size_t)min(m0 + row, p.M - 1) * p.lda + col;  // rows past M repeat row M-1
+    aoff[i] = (uint32_t)min(row, p.M - 1 - m0) * (uint32_t)p.lda + col;  // rows past M repeat row M-1
     a_lds[i] = row * LDK + col;
   }
 
@@ -435,16 +437,17 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   const int nk = p.K / BK;
   auto load_a = [&](int kt, AStage& a) {
     kt = min(kt, nk - 1);
+    const half* at = abase + kt * BK;
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) a.v[i] = *reinterpret_cast<const uint4*>(arow[i] + kt * BK);
+    for (int i = 0; i < A_CH; ++i) a.v[i] = *reinterpret_cast<const uint4*>(at + aoff[i]);
   };
   auto load_b = [&](int kt, BStage& b) {
     kt = min(kt, nk - 1);
+    const uint8_t* bt = bbase + (size_t)kt * B_TILE_BYTES;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int q = 0; q < B_V / 2; ++q)
-        b.v[j * (B_V / 2) + q] = *reinterpret_cast<const uint4*>(brow[j] + (size_t)kt * B_TILE_BYTES + 16 * q);
+      for (int q = 0; q < B_V / 2; ++q) b.v[j * (B_V / 2) + q] = *reinterpret_cast<const uint4*>(bt + boff[j] + 16 * q);
   };
   auto store_chunk = [&](int buf, const AStage& a, int i) {
     if constexpr (ABF16) {
@@ -492,14 +495,20 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   auto tile = [&](int cur, int nxt, const BStage& bs, const AStage& as) {
     half8 af[2][FM];
     half8 bf[2][2];
+    constexpr int VEXP = LUT4 ? 50 : 1;  // VALU instructions of two code expansions
+    constexpr int VPER = (VEXP + 2 * FM - 1) / (2 * FM);
     read_af(af[0], cur, 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j) bf[0][j] = b_frag(bs, j, 0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int c = s & 1, n = c ^ 1;
+      // slice s+1's fragment reads are issued before slice s's MFMAs (the
+      // scheduler would otherwise sink them next to their use); the MFMAs
+      // interleave with slice s+1's code expansions
+      if (s < 3) read_af(af[n], cur, s + 1);
+      __builtin_amdgcn_sched_barrier(0);
       if (s < 3) {
-        read_af(af[n], cur, s + 1);
 #pragma unroll
         for (int j = 0; j < 2; ++j) bf[n][j] = b_frag(bs, j, s + 1);
       }
@@ -511,15 +520,12 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
-      if (s < 3) {
-        constexpr int VPER = LUT4 ? (52 + 2 * FM - 1) / (2 * FM) : 1;
-        __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);
 #pragma unroll
-        for (int m = 0; m < 2 * FM; ++m) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x002, VPER, 0);
-        }
+      for (int m = 0; m < 2 * FM; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (s < 3) __builtin_amdgcn_sched_group_barrier(0x002, VPER, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -531,28 +537,28 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   load_b(0, rb0);
   load_a(1, ra1);
   load_b(1, rb1);
-  load_a(2, ra2);
+  if constexpr (AD == 4) load_a(2, ra2);
   if constexpr (LUT4) load_b(2, rb2);
-  load_a(3, ra3);
+  if constexpr (AD == 4) load_a(3, ra3);
   if constexpr (LUT4) load_b(3, rb3);
 #pragma unroll
   for (int i = 0; i < A_CH; ++i) store_chunk(0, ra0, i);
   __syncthreads();
   for (int kt = 0; kt < nk; kt += 4) {
     tile(0, 1, rb0, ra1);
-    load_a(kt + 4, ra0);
+    load_a(kt + AD, ra0);
     load_b(kt + BD, rb0);
     __syncthreads();
-    tile(1, 0, rb1, ra2);
-    load_a(kt + 5, ra1);
+    tile(1, 0, rb1, AD == 4 ? ra2 : ra0);
+    load_a(kt + 1 + AD, ra1);
     load_b(kt + 1 + BD, rb1);
     __syncthreads();
-    tile(0, 1, LUT4 ? rb2 : rb0, ra3);
-    load_a(kt + 6, ra2);
+    tile(0, 1, LUT4 ? rb2 : rb0, AD == 4 ? ra3 : ra1);
+    load_a(kt + 2 + AD, AD == 4 ? ra2 : ra0);
     load_b(kt + 2 + BD, LUT4 ? rb2 : rb0);
     __syncthreads();
     tile(1, 0, LUT4 ? rb3 : rb1, ra0);
-    load_a(kt + 7, ra3);
+    load_a(kt + 3 + AD, AD == 4 ? ra3 : ra1);
     load_b(kt + 3 + BD, LUT4 ? rb3 : rb1);
     __syncthreads();
   }
@@ -671,16 +677,20 @@ int pick_bm(int M, int N) {
   return (tiles128 >= 256 && N < 4096) ? 128 : 64;
 }
 
-// 32-row MFMA blocks per wide tile (0 = use the 128-column kernel). Four
-// (128-row tiles) when that makes at least half a launch of one workgroup per
-// CU without a second, mostly idle round, two otherwise; from a sweep of the
-// encoder shapes on MI355X. BARK_HIP_GEMM_WIDE = 0/2/4 forces a choice.
+// 32-row MFMA blocks per wide tile (0 = use the 128-column kernel), from a
+// sweep of the encoder shapes on MI355X: eight (256-row tiles, half the code
+// expansions per MFMA) once they fill the CUs at least once, four when
+// 128-row tiles give at least half a launch of one workgroup per CU without a
+// second, mostly idle round, two otherwise. BARK_HIP_GEMM_WIDE = 0/2/4/8
+// forces a choice.
 int pick_wide_fm(int M, int N) {
   static const int forced = [] {
     const char* e = getenv("BARK_HIP_GEMM_WIDE");
     return e ? atoi(e) : -1;
   }();
-  if (forced == 0 || forced == 2 || forced == 4) return forced;
+  if (forced == 0 || forced == 2 || forced == 4 || forced == 8) return forced;
+  const long tiles8 = (long)ceil_div(M, 256) * (N / 256);
+  if (tiles8 >= 256) return 8;
   const long tiles4 = (long)ceil_div(M, 128) * (N / 256);
   return (tiles4 >= 128 && (tiles4 <= 256 || tiles4 >= 512)) ? 4 : 2;
 }
@@ -709,10 +719,12 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   BARK_REQUIRE(W.lut4() ? (W.lut != nullptr) : (W.w16 != nullptr), "gemm: weight not set");
   GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea};
   BARK_REQUIRE(!a_bf16 || (W.lut4() && !W.swizzled), "gemm: bf16 activations need plain 4-bit weights");
-  const int fm = W.n % 256 == 0 ? pick_wide_fm(M, W.n) : 0;
+  const bool fits32 = (double)M * lda * 2 < 4.0e9 && (double)W.n * W.k * 2 < 4.0e9;
+  const int fm = W.n % 256 == 0 && fits32 ? pick_wide_fm(M, W.n) : 0;
   if (fm) {
     const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
-    if (fm == 4) launch_wide<4>(p, epi, fmt, a_bf16, stream);
+    if (fm == 8) launch_wide<8>(p, epi, fmt, a_bf16, stream);
+    else if (fm == 4) launch_wide<4>(p, epi, fmt, a_bf16, stream);
     else launch_wide<2>(p, epi, fmt, a_bf16, stream);
     BARK_HIP_CHECK(hipGetLastError());
     return;
