@@ -204,6 +204,7 @@ struct BarkHip {
 
   // workspace
   DevBuf sub16, xn, hid, qu, qv, kh, vt, rk, ao, h, h2, glu, pooler, dump, bounds, tiles;
+  DevBuf part;  // split-K partial sums of the residual linears
   DevBuf y1, y2, y3, y4, mel, subf32;
 
   template <class T>
@@ -225,13 +226,16 @@ struct BarkHip {
     const size_t want = (bytes + 4095) & ~size_t(4095);
     BARK_HIP_CHECK(hipMalloc(&b.p, want));
     BARK_HIP_CHECK(hipMemset(b.p, 0, want));
+    // the fill runs on the null stream, which the library's non-blocking
+    // streams do not wait for: finish it before anything is queued after it
+    BARK_HIP_CHECK(hipDeviceSynchronize());
     b.cap = want;
   }
 
   ~BarkHip() {
     if (stream) (void)hipStreamSynchronize(stream);
     for (void* p : allocs) (void)hipFree(p);
-    DevBuf* bufs[] = {&pos, &sub16, &xn, &hid, &qu, &qv, &kh, &vt, &rk, &ao, &h, &h2, &glu,
+    DevBuf* bufs[] = {&pos, &sub16, &xn, &hid, &qu, &qv, &kh, &vt, &rk, &ao, &h, &h2, &glu, &part,
                       &pooler, &dump, &bounds, &tiles, &y1, &y2, &y3, &y4, &mel, &subf32};
     for (DevBuf* b : bufs)
       if (b->p) (void)hipFree(b->p);
@@ -495,6 +499,8 @@ struct BarkHip {
     ensure(h, mp * HIDDEN * 4);
     ensure(h2, mp * HIDDEN * 4);
     ensure(glu, mp * HIDDEN * 4);
+    ensure(part, (size_t)std::max(residual_splits(HIDDEN, HIDDEN), residual_splits(HIDDEN, FFN)) * mp *
+                     HIDDEN * 4);
     ensure(pooler, mp * PROJ * 4);
     ensure(bounds, mp * sizeof(int2));
     ensure(tiles, (mp / 64 + pl.seqs.size()) * sizeof(int4));
@@ -537,6 +543,23 @@ struct BarkHip {
     const double flops = 2.0 * m_real * W.n * W.k;
     const double bytes = weight_bytes(W) + 2.0 * m_real * W.k + out_bytes_per_row * m_real;
     prof.run(label, flops, bytes, st, [&] { gemm(A, lda, M, W, epi, e, st); });
+  }
+
+  // A residual linear (N = 1024) as split-K partial sums into `part`; the
+  // returned update is applied by the LayerNorm that follows it.
+  ResidIn resid_op(const char* label, const half* A, int lda, int M, int m_real, const GemmWeight& W,
+                   float scale, hipStream_t st) {
+    const int splits = residual_splits(W.n, W.k);
+    const double flops = 2.0 * m_real * W.n * W.k;
+    const double bytes = weight_bytes(W) + 2.0 * m_real * W.k + 4.0 * splits * m_real * W.n;
+    prof.run(label, flops, bytes, st,
+             [&] { gemm_split(A, lda, M, W, splits, part.as<float>(), HIDDEN, st); });
+    ResidIn r;
+    r.part = part.as<float>();
+    r.splits = splits;
+    r.stride = (size_t)M * HIDDEN;
+    r.scale = scale;
+    return r;
   }
 
   // conv front end of one utterance into rows [s.start, s.start+s.t) of sub16.
@@ -617,18 +640,15 @@ struct BarkHip {
       if (l == 0)
         prof.run("layernorm", 0, ln_bytes, st,
                  [&] { layer_norm(hc, L.ln_w[0], L.ln_b[0], xnp, nullptr, mp, st); });
-      // ---- FF1: h += 0.5 * W2 silu(W1 LN(h))
+      // ---- FF1: h += 0.5 * W2 silu(W1 LN(h)); the residual add happens in the next LN
       EpiArgs e;
       e.out_f16 = hid.as<half>();
       e.ldo = FFN;
       gemm_op("ff_up_silu", xnp, HIDDEN, mp, mr, L.ff1a, Epi::Silu, e, 2.0 * FFN, st);
-      e = EpiArgs();
-      e.out_f32 = hc;
-      e.ldo = HIDDEN;
-      gemm_op("ff_down_resid", hid.as<half>(), FFN, mp, mr, L.ff1b, Epi::ResidHalf, e, 8.0 * HIDDEN, st);
+      ResidIn res = resid_op("ff_down_resid", hid.as<half>(), FFN, mp, mr, L.ff1b, 0.5f, st);
       // ---- attention
-      prof.run("layernorm", 0, ln_bytes, st,
-               [&] { layer_norm(hc, L.ln_w[1], L.ln_b[1], xnp, nullptr, mp, st); });
+      prof.run("layernorm_resid", 0, ln_bytes + 4.0 * (res.splits + 1) * mr * HIDDEN, st,
+               [&] { layer_norm(hc, L.ln_w[1], L.ln_b[1], xnp, nullptr, mp, st, res); });
       e = EpiArgs();
       e.qu = qu.as<half>();
       e.qv = qv.as<half>();
@@ -644,14 +664,10 @@ struct BarkHip {
                   ao.as<half>(), mp, pp, tc, tiles.as<int4>(), ntiles};
       prof.run("rel_attention", attn_flops, 2.0 * mr * HIDDEN * 5 + 2.0 * prows * HIDDEN, st,
                [&] { rel_attention(aa, st); });
-      e = EpiArgs();
-      e.out_f32 = hc;
-      e.ldo = HIDDEN;
-      e.scale = 1.0f;
-      gemm_op("attn_out_resid", ao.as<half>(), HIDDEN, mp, mr, L.o, Epi::Resid, e, 8.0 * HIDDEN, st);
+      res = resid_op("attn_out_resid", ao.as<half>(), HIDDEN, mp, mr, L.o, 1.0f, st);
       // ---- conv module
-      prof.run("layernorm", 0, ln_bytes, st,
-               [&] { layer_norm(hc, L.ln_w[2], L.ln_b[2], xnp, nullptr, mp, st); });
+      prof.run("layernorm_resid", 0, ln_bytes + 4.0 * (res.splits + 1) * mr * HIDDEN, st,
+               [&] { layer_norm(hc, L.ln_w[2], L.ln_b[2], xnp, nullptr, mp, st, res); });
       e = EpiArgs();
       e.out_f32 = glu.as<float>();
       e.ldo = HIDDEN;
@@ -659,35 +675,31 @@ struct BarkHip {
       prof.run("dwconv_bn_silu", 2.0 * 9 * mr * HIDDEN, (double)mr * HIDDEN * 6 + 9 * HIDDEN * 4.0, st, [&] {
         dwconv_bn_silu(glu.as<float>(), L.dw, L.bn_a, L.bn_b, bounds.as<int2>(), xnp, mp, st);
       });
-      e = EpiArgs();
-      e.out_f32 = hc;
-      e.ldo = HIDDEN;
-      e.scale = 1.0f;
-      gemm_op("pw2_resid", xnp, HIDDEN, mp, mr, L.pw2, Epi::Resid, e, 8.0 * HIDDEN, st);
+      res = resid_op("pw2_resid", xnp, HIDDEN, mp, mr, L.pw2, 1.0f, st);
       // ---- FF2
-      prof.run("layernorm", 0, ln_bytes, st,
-               [&] { layer_norm(hc, L.ln_w[3], L.ln_b[3], xnp, nullptr, mp, st); });
+      prof.run("layernorm_resid", 0, ln_bytes + 4.0 * (res.splits + 1) * mr * HIDDEN, st,
+               [&] { layer_norm(hc, L.ln_w[3], L.ln_b[3], xnp, nullptr, mp, st, res); });
       e = EpiArgs();
       e.out_f16 = hid.as<half>();
       e.ldo = FFN;
       gemm_op("ff_up_silu", xnp, HIDDEN, mp, mr, L.ff2a, Epi::Silu, e, 2.0 * FFN, st);
-      e = EpiArgs();
-      e.out_f32 = hc;
-      e.ldo = HIDDEN;
-      gemm_op("ff_down_resid", hid.as<half>(), FFN, mp, mr, L.ff2b, Epi::ResidHalf, e, 8.0 * HIDDEN, st);
-      if (l == dump_layer) {
+      res = resid_op("ff_down_resid", hid.as<half>(), FFN, mp, mr, L.ff2b, 0.5f, st);
+      if (l == dump_layer) {  // the pre-norm residual of this block
+        apply_residual(hc, mp, res, st);
+        res = ResidIn();
         ensure(dump, (size_t)mp * HIDDEN * 4);
         copy_rows_f32(hc, HIDDEN, dump.as<float>(), HIDDEN, mp, HIDDEN, st);
       }
       // ---- norm_out (fused with the next block's first LayerNorm)
+      const double rb = 4.0 * (res.splits ? res.splits : 0) * mr * HIDDEN;
       if (l + 1 < n_layers) {
         const DevLayer& N = layers[l + 1];
-        prof.run("layernorm_pair", 0, (double)mr * HIDDEN * (4 + 4 + 2), st, [&] {
-          layer_norm2(hc, L.ln_w[4], L.ln_b[4], ha, N.ln_w[0], N.ln_b[0], xnp, mp, st);
+        prof.run("layernorm_pair", 0, (double)mr * HIDDEN * (4 + 4 + 2) + rb, st, [&] {
+          layer_norm2(hc, L.ln_w[4], L.ln_b[4], ha, N.ln_w[0], N.ln_b[0], xnp, mp, st, res);
         });
       } else {
-        prof.run("layernorm", 0, (double)mr * HIDDEN * (4 + 4 + 2), st,
-                 [&] { layer_norm(hc, L.ln_w[4], L.ln_b[4], xnp, ha, mp, st); });
+        prof.run("layernorm_resid", 0, (double)mr * HIDDEN * (4 + 4 + 2) + rb, st,
+                 [&] { layer_norm(hc, L.ln_w[4], L.ln_b[4], xnp, ha, mp, st, res); });
       }
       std::swap(hc, ha);
     }

@@ -44,6 +44,8 @@ struct GemmParams {
   const half* lut;
   int M, N, K;
   EpiArgs ea;
+  int kc = 0;            // wide kernel: k per split (blockIdx.z selects the chunk)
+  size_t out_zstride = 0;  // wide kernel: elements between the splits' outputs
 };
 
 __device__ inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -400,11 +402,12 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   const int l32 = lane & 31, lhi = lane >> 5;
   const int n0 = blockIdx.x * 256, m0 = blockIdx.y * BM;
   const int nw = n0 + wid * 64;
+  const int kz0 = blockIdx.z * p.kc;  // first k of this split
 
   // Global addresses are a wave-uniform base plus 32-bit lane offsets (the
   // host checks the operands fit), so loads use scalar base registers.
   RowLut lut[2];
-  const uint8_t* bbase = LUT4 ? p.codes : reinterpret_cast<const uint8_t*>(p.W);
+  const uint8_t* bbase = LUT4 ? p.codes + kz0 / 2 : reinterpret_cast<const uint8_t*>(p.W + kz0);
   constexpr int B_ROW_BYTES_PER_K2 = LUT4 ? 1 : 4;  // bytes per row per 2 k
   uint32_t boff[2];  // this lane's B bytes of k-tile 0, for its two rows
 #pragma unroll
@@ -414,7 +417,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
     boff[j] = (uint32_t)n * (uint32_t)(p.K / 2 * B_ROW_BYTES_PER_K2) + (LUT4 ? 16 : 64) * lhi;
   }
   constexpr int B_TILE_BYTES = LUT4 ? BK / 2 : BK * 2;
-  const half* abase = p.A + (size_t)m0 * p.lda;
+  const half* abase = p.A + (size_t)m0 * p.lda + kz0;
   uint32_t aoff[A_CH];
   int a_lds[A_CH];
 #pragma unroll
@@ -434,7 +437,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   BStage rb0, rb1, rb2, rb3;  // f16 mode uses rb0/rb1 only
 
   // Loads past the last k-tile re-read it (no branch, stays in bounds).
-  const int nk = p.K / BK;
+  const int nk = p.kc / BK;
   auto load_a = [&](int kt, AStage& a) {
     kt = min(kt, nk - 1);
     const half* at = abase + kt * BK;
@@ -563,7 +566,8 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
     __syncthreads();
   }
 
-  const EpiArgs& ea = p.ea;
+  EpiArgs ea = p.ea;
+  if constexpr (EPI == (int)Epi::StoreF32) ea.out_f32 += blockIdx.z * p.out_zstride;
   if constexpr (EPI == (int)Epi::Glu) {
     const int c = (nw >> 1) + l32;
 #pragma unroll
@@ -591,7 +595,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
 // (isolated linear; f16 or bf16 activations).
 template <int FM>
 void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t s) {
-  dim3 grid(p.N / 256, ceil_div(p.M, 32 * FM)), block(256);
+  dim3 grid(p.N / 256, ceil_div(p.M, 32 * FM), p.K / p.kc), block(256);
 #define BARK_K(L4, SW, AB, E) \
   hipLaunchKernelGGL((gemm_wide_kernel<FM, L4, SW, AB, (int)Epi::E>), grid, block, 0, s, p)
 #define BARK_CASE(E)                                   \
@@ -683,15 +687,15 @@ int pick_bm(int M, int N) {
 // 128-row tiles give at least half a launch of one workgroup per CU without a
 // second, mostly idle round, two otherwise. BARK_HIP_GEMM_WIDE = 0/2/4/8
 // forces a choice.
-int pick_wide_fm(int M, int N) {
+int pick_wide_fm(int M, int N, int splits = 1) {
   static const int forced = [] {
     const char* e = getenv("BARK_HIP_GEMM_WIDE");
     return e ? atoi(e) : -1;
   }();
   if (forced == 0 || forced == 2 || forced == 4 || forced == 8) return forced;
-  const long tiles8 = (long)ceil_div(M, 256) * (N / 256);
+  const long tiles8 = (long)ceil_div(M, 256) * (N / 256) * splits;
   if (tiles8 >= 256) return 8;
-  const long tiles4 = (long)ceil_div(M, 128) * (N / 256);
+  const long tiles4 = (long)ceil_div(M, 128) * (N / 256) * splits;
   return (tiles4 >= 128 && (tiles4 <= 256 || tiles4 >= 512)) ? 4 : 2;
 }
 
@@ -717,7 +721,7 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   BARK_REQUIRE(M > 0, "gemm: M must be positive");
   BARK_REQUIRE(lda >= W.k && lda % 8 == 0, "gemm: lda must be >= K and a multiple of 8");
   BARK_REQUIRE(W.lut4() ? (W.lut != nullptr) : (W.w16 != nullptr), "gemm: weight not set");
-  GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea};
+  GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, W.k, 0};
   BARK_REQUIRE(!a_bf16 || (W.lut4() && !W.swizzled), "gemm: bf16 activations need plain 4-bit weights");
   const bool fits32 = (double)M * lda * 2 < 4.0e9 && (double)W.n * W.k * 2 < 4.0e9;
   const int fm = W.n % 256 == 0 && fits32 ? pick_wide_fm(M, W.n) : 0;
@@ -741,6 +745,49 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   BARK_BM(64)
 #undef BARK_BM
   BARK_HIP_CHECK(hipGetLastError());
+}
+
+void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, float* part,
+                int ldo, hipStream_t stream) {
+  BARK_REQUIRE(A != nullptr && part != nullptr, "gemm_split: null operand");
+  BARK_REQUIRE(splits >= 1 && W.k % splits == 0 && (W.k / splits) % (4 * BK) == 0,
+               "gemm_split: K / splits must be a positive multiple of 256");
+  BARK_REQUIRE(W.n % 256 == 0 && W.n > 0, "gemm_split: N must be a positive multiple of 256");
+  BARK_REQUIRE(M > 0 && ldo >= W.n, "gemm_split: bad M or ldo");
+  BARK_REQUIRE(lda >= W.k && lda % 8 == 0, "gemm_split: lda must be >= K and a multiple of 8");
+  BARK_REQUIRE(W.lut4() ? (W.lut != nullptr) : (W.w16 != nullptr), "gemm_split: weight not set");
+  BARK_REQUIRE((double)M * lda * 2 < 4.0e9 && (double)W.n * W.k * 2 < 4.0e9,
+               "gemm_split: operand too large for 32-bit offsets");
+  EpiArgs ea;
+  ea.out_f32 = part;
+  ea.ldo = ldo;
+  GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, W.k / splits, (size_t)M * ldo};
+  const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
+  int fm = pick_wide_fm(M, W.n, splits);
+  if (fm == 0) fm = 2;
+  if (fm == 8) launch_wide<8>(p, Epi::StoreF32, fmt, false, stream);
+  else if (fm == 4) launch_wide<4>(p, Epi::StoreF32, fmt, false, stream);
+  else launch_wide<2>(p, Epi::StoreF32, fmt, false, stream);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
+// From a sweep of the N = 1024 residual linears at T = 2207 on MI355X.
+// BARK_HIP_SPLIT_K1 / BARK_HIP_SPLIT_K4 override the count for K = 1024 /
+// K = 4096.
+int residual_splits(int n, int k) {
+  static const int f1 = [] {
+    const char* e = getenv("BARK_HIP_SPLIT_K1");
+    return e ? atoi(e) : 0;
+  }();
+  static const int f4 = [] {
+    const char* e = getenv("BARK_HIP_SPLIT_K4");
+    return e ? atoi(e) : 0;
+  }();
+  int s = 1;
+  if (n == 1024 && k == 1024) s = f1 ? f1 : 2;
+  if (n == 1024 && k == 4096) s = f4 ? f4 : 2;
+  while (s > 1 && (k % s != 0 || (k / s) % 256 != 0)) --s;
+  return s;
 }
 
 }  // namespace bark

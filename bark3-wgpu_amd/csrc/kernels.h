@@ -59,6 +59,25 @@ void swizzle_codes(uint8_t* codes, size_t nbytes);
 void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const EpiArgs& ea,
           hipStream_t stream, bool a_bf16 = false);
 
+// Split-K GEMM into partial sums: K is cut into `splits` equal chunks (each a
+// multiple of 256) and chunk s writes its f32 product to
+// part + s * M * ldo (row stride ldo). The consumer adds the chunks in order
+// s = 0, 1, ... (see ResidIn), so the result depends on (N, K, splits) only,
+// never on M or on which workgroup finished first.
+void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, float* part,
+                int ldo, hipStream_t stream);
+// Split-K count for the residual linears, a function of (N, K) only.
+int residual_splits(int n, int k);
+
+// Deferred residual update read by the LayerNorm kernels: x += scale * (p_0 +
+// p_1 + ... ) with p_s = part + s * stride, summed in that order.
+struct ResidIn {
+  const float* part = nullptr;
+  int splits = 0;  // 0: no pending update
+  size_t stride = 0;
+  float scale = 1.0f;
+};
+
 // ----------------------------------------------------------- attention --
 // One entry per 128-query tile: {row of the sequence's first frame, sequence
 // length, first query of the tile (local), 0}.
@@ -77,12 +96,18 @@ void rel_attention(const AttnArgs& a, hipStream_t stream);
 float attention_q_scale();
 
 // ----------------------------------------------------------------- ops --
-// LayerNorm over 1024 columns. y16 and/or y32 may be null.
-void layer_norm(const float* x, const float* w, const float* b, half* y16, float* y32,
-                int rows, hipStream_t stream);
-// y32 = LN_a(x) (written), y16 = f16(LN_b(y32)).
+// LayerNorm over 1024 columns. y16 and/or y32 may be null. With a pending
+// residual update `res`, x is first updated in place (x += res) and the norm
+// is taken of the updated rows.
+void layer_norm(float* x, const float* w, const float* b, half* y16, float* y32,
+                int rows, hipStream_t stream, const ResidIn& res = ResidIn());
+// y32 = LN_a(x + res) (written), y16 = f16(LN_b(y32)); x itself is not
+// updated (the residual stream continues in y32).
 void layer_norm2(const float* x, const float* wa, const float* ba, float* y32,
-                 const float* wb, const float* bb, half* y16, int rows, hipStream_t stream);
+                 const float* wb, const float* bb, half* y16, int rows, hipStream_t stream,
+                 const ResidIn& res = ResidIn());
+// x += res in place (rows x 1024).
+void apply_residual(float* x, int rows, const ResidIn& res, hipStream_t stream);
 // out = f16(silu(BN(dwconv9(g)))) with per-row [start, end) frame bounds.
 void dwconv_bn_silu(const float* g, const float* dw, const float* bn_a, const float* bn_b,
                     const int2* bounds, half* out, int rows, hipStream_t stream);

@@ -57,27 +57,57 @@ __device__ inline void store_row16(half* y, const float (&v)[16], int lane) {
   }
 }
 
-__global__ void __launch_bounds__(256) ln_kernel(const float* x, const float* w, const float* b,
-                                                 half* y16, float* y32, int rows) {
+// x += scale * (p_0 + p_1 + ...), partial sums added in split order.
+__device__ inline void add_residual(float (&v)[16], const ResidIn& res, size_t row_off, int lane) {
+  float p[16];
+  load_row(res.part + row_off, p, lane);
+  for (int s = 1; s < res.splits; ++s) {
+    float q[16];
+    load_row(res.part + s * res.stride + row_off, q, lane);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] += q[i];
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = v[i] + res.scale * p[i];
+}
+
+__global__ void __launch_bounds__(256) ln_kernel(float* x, const float* w, const float* b,
+                                                 half* y16, float* y32, int rows, ResidIn res) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   float v[16];
   load_row(x + (size_t)r * HIDDEN, v, lane);
+  if (res.splits) {
+    add_residual(v, res, (size_t)r * HIDDEN, lane);
+    store_row32(x + (size_t)r * HIDDEN, v, lane);
+  }
   ln_row(v, w, b, lane);
   if (y32) store_row32(y32 + (size_t)r * HIDDEN, v, lane);
   if (y16) store_row16(y16 + (size_t)r * HIDDEN, v, lane);
 }
 
-// Block-final norm_out of layer l fused with norm_feed_forward1 of layer l+1.
-__global__ void __launch_bounds__(256) ln2_kernel(const float* x, const float* wa,
-                                                  const float* ba, float* y32, const float* wb,
-                                                  const float* bb, half* y16, int rows) {
+__global__ void __launch_bounds__(256) resid_kernel(float* x, int rows, ResidIn res) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   float v[16];
   load_row(x + (size_t)r * HIDDEN, v, lane);
+  add_residual(v, res, (size_t)r * HIDDEN, lane);
+  store_row32(x + (size_t)r * HIDDEN, v, lane);
+}
+
+// Block-final norm_out of layer l fused with norm_feed_forward1 of layer l+1.
+__global__ void __launch_bounds__(256) ln2_kernel(const float* x, const float* wa,
+                                                  const float* ba, float* y32, const float* wb,
+                                                  const float* bb, half* y16, int rows,
+                                                  ResidIn res) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  float v[16];
+  load_row(x + (size_t)r * HIDDEN, v, lane);
+  if (res.splits) add_residual(v, res, (size_t)r * HIDDEN, lane);
   ln_row(v, wa, ba, lane);
   store_row32(y32 + (size_t)r * HIDDEN, v, lane);
   ln_row(v, wb, bb, lane);
@@ -216,19 +246,33 @@ __global__ void __launch_bounds__(256) sub_dw_kernel(const half* in, int t_in, i
 
 }  // namespace
 
-void layer_norm(const float* x, const float* w, const float* b, half* y16, float* y32,
-                int rows, hipStream_t stream) {
+static void check_resid(const ResidIn& res) {
+  BARK_REQUIRE(res.splits == 0 || (res.part != nullptr && res.splits > 0 && res.splits <= 16),
+               "residual partials: bad split count or null buffer");
+}
+
+void layer_norm(float* x, const float* w, const float* b, half* y16, float* y32, int rows,
+                hipStream_t stream, const ResidIn& res) {
   if (rows <= 0) return;
+  check_resid(res);
   hipLaunchKernelGGL(ln_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, w, b, y16,
-                     y32, rows);
+                     y32, rows, res);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
 void layer_norm2(const float* x, const float* wa, const float* ba, float* y32, const float* wb,
-                 const float* bb, half* y16, int rows, hipStream_t stream) {
+                 const float* bb, half* y16, int rows, hipStream_t stream, const ResidIn& res) {
   if (rows <= 0) return;
+  check_resid(res);
   hipLaunchKernelGGL(ln2_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, wa, ba,
-                     y32, wb, bb, y16, rows);
+                     y32, wb, bb, y16, rows, res);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
+void apply_residual(float* x, int rows, const ResidIn& res, hipStream_t stream) {
+  if (rows <= 0 || res.splits == 0) return;
+  check_resid(res);
+  hipLaunchKernelGGL(resid_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, rows, res);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
