@@ -395,7 +395,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   constexpr int A_CH = BM * BK / 8 / 256;  // 16-byte chunks of A per thread per k-tile (= FM)
   constexpr int B_V = LUT4 ? 2 : 8;        // 16-byte loads of B per lane per k-tile
   constexpr int BD = LUT4 ? 4 : 2;         // k-tiles of B in flight (register stages)
-  constexpr int AD = FM >= 8 ? 2 : 4;      // k-tiles of A in flight (register stages)
+  constexpr int AD = FM >= 6 ? 2 : 4;      // k-tiles of A in flight (register stages)
   __shared__ __attribute__((aligned(16))) half As[2][BM * LDK];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -592,7 +592,26 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
 }
 
 // Weight format: 0 = f16, 1 = swizzled 4-bit (encoder), 2 = plain 4-bit
-// (isolated linear; f16 or bf16 activations).
+// (isolated linear; f16 or bf16 activations). Only the combinations the
+// encoder and the isolated linear use are instantiated; wide_supported()
+// tells the dispatcher which ones exist (the rest run on the 128-column
+// kernel).
+bool wide_supported(Epi epi, int fmt) {
+  if (fmt == 2) return epi == Epi::StoreF32 || epi == Epi::StoreF16 || epi == Epi::StoreBF16;
+  switch (epi) {
+    case Epi::StoreF32:
+    case Epi::Silu:
+    case Epi::Glu:
+    case Epi::Qkv:
+    case Epi::RelK:
+    case Epi::BiasReluF16:
+    case Epi::FlattenReluF16:
+      return true;
+    default:
+      return false;
+  }
+}
+
 template <int FM>
 void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t s) {
   dim3 grid(p.N / 256, ceil_div(p.M, 32 * FM), p.K / p.kc), block(256);
@@ -601,25 +620,38 @@ void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t 
 #define BARK_CASE(E)                                   \
   case Epi::E:                                         \
     if (fmt == 0) BARK_K(false, false, false, E);      \
-    else if (fmt == 1) BARK_K(true, true, false, E);   \
-    else if (abf16) BARK_K(true, false, true, E);      \
+    else BARK_K(true, true, false, E);                 \
+    return;
+#define BARK_PLAIN(E)                                  \
+  case Epi::E:                                         \
+    if (abf16) BARK_K(true, false, true, E);           \
     else BARK_K(true, false, false, E);                \
-    break;
-  switch (epi) {
-    BARK_CASE(StoreF32)
-    BARK_CASE(StoreF16)
-    BARK_CASE(StoreBF16)
-    BARK_CASE(Silu)
-    BARK_CASE(Resid)
-    BARK_CASE(ResidHalf)
-    BARK_CASE(Glu)
-    BARK_CASE(Qkv)
-    BARK_CASE(RelK)
-    BARK_CASE(BiasReluF16)
-    BARK_CASE(FlattenReluF16)
+    return;
+  if (fmt == 2) {
+    switch (epi) {
+      BARK_PLAIN(StoreF32)
+      BARK_PLAIN(StoreF16)
+      BARK_PLAIN(StoreBF16)
+      default:
+        break;
+    }
+  } else {
+    switch (epi) {
+      BARK_CASE(StoreF32)
+      BARK_CASE(Silu)
+      BARK_CASE(Glu)
+      BARK_CASE(Qkv)
+      BARK_CASE(RelK)
+      BARK_CASE(BiasReluF16)
+      BARK_CASE(FlattenReluF16)
+      default:
+        break;
+    }
   }
+#undef BARK_PLAIN
 #undef BARK_CASE
 #undef BARK_K
+  throw Error{"gemm: no wide kernel for this epilogue and weight format"};
 }
 
 // Full epilogue set: f16 weights and swizzled 4-bit weights (the encoder).
@@ -667,36 +699,36 @@ void launch_plain(const GemmParams& p, Epi epi, bool abf16, hipStream_t s) {
 #undef BARK_CASE
 }
 
-// Rows per workgroup tile, from a sweep of the encoder shapes on MI355X: 128
-// rows when that still gives every CU a workgroup (N = 2048/3072, or long
-// sequences), otherwise 64 (N = 1024 leaves CUs idle at 128 rows; at N = 4096
-// the 64-row tile was marginally faster). BARK_HIP_GEMM_BM forces a height.
-int pick_bm(int M, int N) {
-  static const int forced = [] {
-    const char* e = getenv("BARK_HIP_GEMM_BM");
-    return e ? atoi(e) : 0;
-  }();
-  if (forced == 64 || forced == 128 || forced == 256) return forced;
-  const long tiles128 = (long)ceil_div(M, 128) * (N / BN);
-  return (tiles128 >= 256 && N < 4096) ? 128 : 64;
-}
-
-// 32-row MFMA blocks per wide tile (0 = use the 128-column kernel), from a
-// sweep of the encoder shapes on MI355X: eight (256-row tiles, half the code
-// expansions per MFMA) once they fill the CUs at least once, four when
-// 128-row tiles give at least half a launch of one workgroup per CU without a
-// second, mostly idle round, two otherwise. BARK_HIP_GEMM_WIDE = 0/2/4/8
-// forces a choice.
-int pick_wide_fm(int M, int N, int splits = 1) {
+// 32-row MFMA blocks per wide tile (0 = use the 128-column kernel). Taller
+// tiles spend fewer code expansions per MFMA but make fewer workgroups, so
+// each height is scored as (fraction of the CU slots its launch keeps busy,
+// counting every round) x (its relative per-CU rate); the best score wins.
+// Two-block tiles run two workgroups per CU once there are more than one per
+// CU. Rates and the short-K rule are from sweeps of the encoder shapes on
+// MI355X. BARK_HIP_GEMM_WIDE = 0/2/4/6/8 forces a choice.
+int pick_wide_fm(int M, int N, int K, int splits = 1) {
   static const int forced = [] {
     const char* e = getenv("BARK_HIP_GEMM_WIDE");
     return e ? atoi(e) : -1;
   }();
-  if (forced == 0 || forced == 2 || forced == 4 || forced == 8) return forced;
-  const long tiles8 = (long)ceil_div(M, 256) * (N / 256) * splits;
-  if (tiles8 >= 256) return 8;
-  const long tiles4 = (long)ceil_div(M, 128) * (N / 256) * splits;
-  return (tiles4 >= 128 && (tiles4 <= 256 || tiles4 >= 512)) ? 4 : 2;
+  if (forced == 0 || forced == 2 || forced == 4 || forced == 6 || forced == 8) return forced;
+  constexpr int CUS = 256;
+  if (K / splits <= 256) return 2;  // a few k-tiles: the prologue dominates
+  int best = 2;
+  double best_score = -1.0;
+  const int fms[4] = {2, 4, 6, 8};
+  const double rate[4] = {0.9, 1.0, 1.1, 1.15};
+  for (int i = 0; i < 4; ++i) {
+    const long tiles = (long)ceil_div(M, 32 * fms[i]) * (N / 256) * splits;
+    const long slots = (fms[i] == 2 && tiles > CUS) ? 2 * CUS : CUS;
+    const long rounds = (tiles + slots - 1) / slots;
+    const double score = (double)tiles / (double)(slots * rounds) * rate[i];
+    if (score > best_score + 1e-9) {
+      best_score = score;
+      best = fms[i];
+    }
+  }
+  return best;
 }
 
 }  // namespace
@@ -724,26 +756,21 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, W.k, 0};
   BARK_REQUIRE(!a_bf16 || (W.lut4() && !W.swizzled), "gemm: bf16 activations need plain 4-bit weights");
   const bool fits32 = (double)M * lda * 2 < 4.0e9 && (double)W.n * W.k * 2 < 4.0e9;
-  const int fm = W.n % 256 == 0 && fits32 ? pick_wide_fm(M, W.n) : 0;
+  const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
+  const int fm = W.n % 256 == 0 && fits32 && wide_supported(epi, fmt) ? pick_wide_fm(M, W.n, W.k) : 0;
   if (fm) {
-    const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
     if (fm == 8) launch_wide<8>(p, epi, fmt, a_bf16, stream);
+    else if (fm == 6) launch_wide<6>(p, epi, fmt, a_bf16, stream);
     else if (fm == 4) launch_wide<4>(p, epi, fmt, a_bf16, stream);
     else launch_wide<2>(p, epi, fmt, a_bf16, stream);
     BARK_HIP_CHECK(hipGetLastError());
     return;
   }
-  const int bm = pick_bm(M, W.n);
-#define BARK_BM(BMV)                                             \
-  if (bm == BMV) {                                               \
-    if (!W.lut4()) launch_full<BMV, false, false>(p, epi, stream); \
-    else if (W.swizzled) launch_full<BMV, true, true>(p, epi, stream); \
-    else launch_plain<BMV>(p, epi, a_bf16, stream);              \
-  }
-  BARK_BM(256)
-  BARK_BM(128)
-  BARK_BM(64)
-#undef BARK_BM
+  // N % 256 != 0 (the projector, narrow isolated linears) or an epilogue
+  // without a wide instance: the 128-column kernel
+  if (!W.lut4()) launch_full<64, false, false>(p, epi, stream);
+  else if (W.swizzled) launch_full<64, true, true>(p, epi, stream);
+  else launch_plain<64>(p, epi, a_bf16, stream);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
@@ -763,9 +790,10 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
   ea.ldo = ldo;
   GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, W.k / splits, (size_t)M * ldo};
   const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
-  int fm = pick_wide_fm(M, W.n, splits);
+  int fm = pick_wide_fm(M, W.n, W.k, splits);
   if (fm == 0) fm = 2;
   if (fm == 8) launch_wide<8>(p, Epi::StoreF32, fmt, false, stream);
+  else if (fm == 6) launch_wide<6>(p, Epi::StoreF32, fmt, false, stream);
   else if (fm == 4) launch_wide<4>(p, Epi::StoreF32, fmt, false, stream);
   else launch_wide<2>(p, Epi::StoreF32, fmt, false, stream);
   BARK_HIP_CHECK(hipGetLastError());
