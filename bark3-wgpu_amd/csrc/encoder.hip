@@ -1021,17 +1021,10 @@ int bark_hip_lowbit_linear(const void* A, int32_t a_dtype, const uint8_t* codes,
     w.lut = reinterpret_cast<const half*>(lut16);
     w.n = N;
     w.k = K;
-    EpiArgs e;
-    e.ldo = N;
-    Epi epi = Epi::StoreF32;
-    if (c_dtype == 0) {
-      e.out_f32 = static_cast<float*>(C);
-    } else {
-      e.out_f16 = static_cast<half*>(C);
-      epi = c_dtype == 1 ? Epi::StoreF16 : Epi::StoreBF16;
-    }
-    gemm(static_cast<const half*>(A), K, T, w, epi, e, static_cast<hipStream_t>(stream),
-         a_dtype == 1);
+    BARK_REQUIRE(K % 256 == 0 && K > 0, "K must be a positive multiple of 256");
+    BARK_REQUIRE(N % 128 == 0 && N > 0, "N must be a positive multiple of 128");
+    gemm_isolated(static_cast<const half*>(A), T, w, C, c_dtype, static_cast<hipStream_t>(stream),
+                  a_dtype == 1);
   });
 }
 

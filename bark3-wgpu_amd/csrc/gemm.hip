@@ -26,6 +26,9 @@
 // into natural k order with half the permutes. Encoder weights are swizzled
 // once at load.
 #include <cstdlib>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "kernels.h"
 
@@ -591,6 +594,35 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   }
 }
 
+// out[r][c] = sum_s part[s][r][c] (s ascending), stored as f32 / f16 / bf16
+// (out_kind 0 / 1 / 2, bf16 rounded to nearest even). Four columns per thread.
+__global__ void __launch_bounds__(256) split_reduce_kernel(const float* part, int splits, size_t stride,
+                                                           void* out, int out_kind, long n4) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  floatx4 v = reinterpret_cast<const floatx4*>(part)[i];
+  for (int s = 1; s < splits; ++s) {
+    const floatx4 q = reinterpret_cast<const floatx4*>(part + s * stride)[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += q[e];
+  }
+  if (out_kind == 0) {
+    reinterpret_cast<floatx4*>(out)[i] = v;
+  } else if (out_kind == 1) {
+    const half4 h = {(half)v[0], (half)v[1], (half)v[2], (half)v[3]};
+    reinterpret_cast<half4*>(out)[i] = h;
+  } else {
+    uint16_t b[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t u = __float_as_uint(v[e]);
+      u += 0x7fffu + ((u >> 16) & 1u);
+      b[e] = (uint16_t)(u >> 16);
+    }
+    reinterpret_cast<uint2*>(out)[i] = make_uint2(b[0] | ((uint32_t)b[1] << 16), b[2] | ((uint32_t)b[3] << 16));
+  }
+}
+
 // Weight format: 0 = f16, 1 = swizzled 4-bit (encoder), 2 = plain 4-bit
 // (isolated linear; f16 or bf16 activations). Only the combinations the
 // encoder and the isolated linear use are instantiated; wide_supported()
@@ -775,7 +807,7 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
 }
 
 void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, float* part,
-                int ldo, hipStream_t stream) {
+                int ldo, hipStream_t stream, bool a_bf16) {
   BARK_REQUIRE(A != nullptr && part != nullptr, "gemm_split: null operand");
   BARK_REQUIRE(splits >= 1 && W.k % splits == 0 && (W.k / splits) % (4 * BK) == 0,
                "gemm_split: K / splits must be a positive multiple of 256");
@@ -783,6 +815,7 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
   BARK_REQUIRE(M > 0 && ldo >= W.n, "gemm_split: bad M or ldo");
   BARK_REQUIRE(lda >= W.k && lda % 8 == 0, "gemm_split: lda must be >= K and a multiple of 8");
   BARK_REQUIRE(W.lut4() ? (W.lut != nullptr) : (W.w16 != nullptr), "gemm_split: weight not set");
+  BARK_REQUIRE(!a_bf16 || (W.lut4() && !W.swizzled), "gemm_split: bf16 activations need plain 4-bit weights");
   BARK_REQUIRE((double)M * lda * 2 < 4.0e9 && (double)W.n * W.k * 2 < 4.0e9,
                "gemm_split: operand too large for 32-bit offsets");
   EpiArgs ea;
@@ -792,10 +825,10 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
   const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
   int fm = pick_wide_fm(M, W.n, W.k, splits);
   if (fm == 0) fm = 2;
-  if (fm == 8) launch_wide<8>(p, Epi::StoreF32, fmt, false, stream);
-  else if (fm == 6) launch_wide<6>(p, Epi::StoreF32, fmt, false, stream);
-  else if (fm == 4) launch_wide<4>(p, Epi::StoreF32, fmt, false, stream);
-  else launch_wide<2>(p, Epi::StoreF32, fmt, false, stream);
+  if (fm == 8) launch_wide<8>(p, Epi::StoreF32, fmt, a_bf16, stream);
+  else if (fm == 6) launch_wide<6>(p, Epi::StoreF32, fmt, a_bf16, stream);
+  else if (fm == 4) launch_wide<4>(p, Epi::StoreF32, fmt, a_bf16, stream);
+  else launch_wide<2>(p, Epi::StoreF32, fmt, a_bf16, stream);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
@@ -816,6 +849,60 @@ int residual_splits(int n, int k) {
   if (n == 1024 && k == 4096) s = f4 ? f4 : 2;
   while (s > 1 && (k % s != 0 || (k / s) % 256 != 0)) --s;
   return s;
+}
+
+namespace {
+// Partial-sum workspace of the isolated linear, one per (device, stream):
+// grow-only, freed at process exit.
+float* isolated_workspace(hipStream_t stream, size_t bytes) {
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> bufs;
+  int dev = 0;
+  BARK_HIP_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(mu);
+  auto& b = bufs[{dev, stream}];
+  if (b.second < bytes) {
+    BARK_HIP_CHECK(hipStreamSynchronize(stream));  // earlier calls may still read the old one
+    if (b.first) BARK_HIP_CHECK(hipFree(b.first));
+    b.first = nullptr;
+    b.second = 0;
+    BARK_HIP_CHECK(hipMalloc(&b.first, bytes));
+    b.second = bytes;
+  }
+  return static_cast<float*>(b.first);
+}
+}  // namespace
+
+void gemm_isolated(const half* A, int M, const GemmWeight& W, void* C, int c_kind, hipStream_t stream,
+                   bool a_bf16) {
+  BARK_REQUIRE(c_kind >= 0 && c_kind <= 2, "gemm_isolated: bad output kind");
+  // Split K when the output tiles alone leave most CUs idle (small T): the
+  // chunks' partial sums go to a workspace and one pass adds them in order.
+  const long base = (long)ceil_div(M, 64) * (W.n / 256);
+  int splits = 1;
+  if (W.n % 256 == 0 && base < 128) {
+    while (splits * 2 * base <= 256 && W.k % (splits * 2) == 0 && (W.k / (splits * 2)) % 256 == 0) splits *= 2;
+  }
+  if (splits == 1) {
+    EpiArgs e;
+    e.ldo = W.n;
+    Epi epi = Epi::StoreF32;
+    if (c_kind == 0) {
+      e.out_f32 = static_cast<float*>(C);
+    } else {
+      e.out_f16 = static_cast<half*>(C);
+      epi = c_kind == 1 ? Epi::StoreF16 : Epi::StoreBF16;
+    }
+    gemm(A, W.k, M, W, epi, e, stream, a_bf16);
+    return;
+  }
+  const size_t stride = (size_t)M * W.n;
+  float* part = isolated_workspace(stream, splits * stride * sizeof(float));
+  gemm_split(A, W.k, M, W, splits, part, W.n, stream, a_bf16);
+  const long n4 = (long)(stride / 4);
+  hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream, part,
+                     splits, stride, C, c_kind, n4);
+  BARK_HIP_CHECK(hipGetLastError());
 }
 
 }  // namespace bark
