@@ -28,7 +28,9 @@
 // Inputs are f16: K, V and relK exactly as the reference rounds them
 // (src/cpu/ops.rs:258-259, src/cpu/layer.rs:234-247); q+u and q+v rounded to
 // f16 for the MFMA operand. Accumulation and softmax are f32.
+#include <algorithm>
 #include <cmath>
+#include <cstdlib>
 
 #include "kernels.h"
 
@@ -62,8 +64,11 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
   // XCD b % 8: giving head b % 8 to it keeps every query tile of one head on one
   // XCD, whose L2 then holds that head's K, V^T and relK (2.2 MB at T = 2207).
   const int h = blockIdx.x % HEADS;
-  const int4 tile = a.tiles[blockIdx.x / HEADS];
+  const int slot = blockIdx.x / HEADS;
+  const int4 tile = a.tiles[slot];
   const int start = tile.x, T = tile.y, q0 = tile.z;
+  const int k_begin = (tile.w & 0xffff) * BKV, k_end = min(T, (tile.w >> 16) * BKV);
+  const bool complete = k_begin == 0 && k_end == T;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int qg = wid & 3, kh = wid >> 2;
   const int l32 = lane & 31, lhi = lane >> 5;
@@ -113,14 +118,15 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) r_row[i] = (tid + NT * i) >> 4;
 
-  // relK band as a ring of 6 blocks of 32 rows: band row r of key tile t lives
-  // in block ((r >> 5) + 2t) % 6. Each tile only fetches its last 64 rows
-  // (the first 128 are the previous tile's last 128).
-  const int jg00 = a.tc - 1 - (q0 + BQ - 1);  // band origin of tile 0
+  // relK band as a ring of 6 blocks of 32 rows: band row r of this
+  // workgroup's key tile t (t = 0 at k_begin) lives in block ((r >> 5) + 2t) % 6.
+  // Each tile only fetches its last 64 rows (the first 128 are the previous
+  // tile's last 128). The band of the tile at key k0 starts at row jg00 + k0.
+  const int jg00 = a.tc - 1 - (q0 + BQ - 1);
   auto r_ok = [&](int j) { return j >= 0 && j < prows; };
-  for (int i = 0; i < R_CH; ++i) {  // tile 0: all 192 rows
+  for (int i = 0; i < R_CH; ++i) {  // first tile: all 192 rows
     const int ch = tid + NT * i, row = ch >> 4;
-    const int j = jg00 + row;
+    const int j = jg00 + k_begin + row;
     const uint4 v = r_ok(j) ? *reinterpret_cast<const uint4*>(rbase + (size_t)j * HDIM + col16) : zero4;
     *reinterpret_cast<uint4*>(&sm.R[row * KLD + col16]) = v;
   }
@@ -158,7 +164,7 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
         vr[i] = v;
       }
     }
-    const int jn = jg00 + 64 * t + 128;  // first new band row of tile t
+    const int jn = jg00 + k0 + 128;  // first new band row of the tile at k0
     if (jn >= 0 && jn + 64 <= prows) {
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -187,12 +193,12 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
   };
 
   const int rb0 = 96 - 32 * qg + 32 * kh;  // first band row of this wave
-  fetch(0, 0);
+  fetch(k_begin, 0);
   int t = 0;
-  for (int k0 = 0; k0 < T; k0 += BKV, ++t) {
+  for (int k0 = k_begin; k0 < k_end; k0 += BKV, ++t) {
     stage(t);
     __syncthreads();
-    if (k0 + BKV < T) fetch(k0 + BKV, t + 1);
+    if (k0 + BKV < k_end) fetch(k0 + BKV, t + 1);
 
     // ---- content scores S^T (this wave's 32 keys x 32 queries) and the
     // position band relK[j] . Qv^T over the wave's 64 band rows: three
@@ -288,7 +294,33 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
     xm[(qg * 2 + 1) * 64 + lane] = l_run;
   }
   __syncthreads();
-  if (kh == 0 && q_lane < T) {
+  if (kh == 0 && !complete) {  // partial over this key range: o unnormalised, with its max and sum
+    const float m1 = xm[(qg * 2) * 64 + lane], l1 = xm[(qg * 2 + 1) * 64 + lane];
+    const float m = fmaxf(m_run, m1);
+    const float c0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+    const float c1 = m1 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m1 - m);
+    const int ql = 32 * qg + l32;
+    const size_t sh = (size_t)slot * HEADS + h;
+    float* po = a.part_o + (sh * BQ + ql) * HDIM;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        floatx4 w4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int v = 4 * g + i;
+          w4[i] = o[db][v] * c0 + xo[(qg * 64 + db * 16 + v) * 64 + lane] * c1;
+        }
+        *reinterpret_cast<floatx4*>(po + 32 * db + 8 * g + 4 * lhi) = w4;
+      }
+    if (lhi == 0) {
+      float* pm = a.part_ml + (sh * BQ + ql) * 2;
+      pm[0] = m;
+      pm[1] = l_run * c0 + l1 * c1;
+    }
+  }
+  if (kh == 0 && complete && q_lane < T) {
     const float m1 = xm[(qg * 2) * 64 + lane], l1 = xm[(qg * 2 + 1) * 64 + lane];
     const float m = fmaxf(m_run, m1);
     const float c0 = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
@@ -310,7 +342,69 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
   }
 }
 
+// Combines the key-range partials of one (query tile, head): with weights
+// w_s = 2^(m_s - max_s m_s), out = sum_s w_s o_s / sum_s w_s l_s, slots in
+// order. Thread t handles query t/2, dims 64*(t&1) .. +63.
+__global__ void __launch_bounds__(256) attn_merge_kernel(const float* part_o, const float* part_ml,
+                                                         const int4* merges, half* out) {
+  const int h = blockIdx.x % HEADS;
+  const int4 mg = merges[blockIdx.x / HEADS];
+  const int q = threadIdx.x >> 1, d0 = (threadIdx.x & 1) * 64;
+  if (q >= mg.w) return;
+  float m = -INFINITY;
+  for (int s = 0; s < mg.y; ++s)
+    m = fmaxf(m, part_ml[(((size_t)(mg.x + s) * HEADS + h) * BQ + q) * 2]);
+  float o[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) o[i] = 0.0f;
+  float l = 0.0f;
+  for (int s = 0; s < mg.y; ++s) {
+    const size_t sh = ((size_t)(mg.x + s) * HEADS + h) * BQ + q;
+    const float w = __builtin_amdgcn_exp2f(part_ml[sh * 2] - m);
+    l += w * part_ml[sh * 2 + 1];
+    const floatx4* src = reinterpret_cast<const floatx4*>(part_o + sh * HDIM + d0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const floatx4 v = src[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[4 * i + e] += w * v[e];
+    }
+  }
+  const float inv = 1.0f / l;
+  half* dst = out + (size_t)(mg.z + q) * HIDDEN + h * HDIM + d0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const half4 w4 = {(half)(o[4 * i] * inv), (half)(o[4 * i + 1] * inv), (half)(o[4 * i + 2] * inv),
+                      (half)(o[4 * i + 3] * inv)};
+    *reinterpret_cast<half4*>(dst + 4 * i) = w4;
+  }
+}
+
 }  // namespace
+
+int attention_splits(int t) {
+  static const int forced = [] {
+    const char* e = getenv("BARK_HIP_ATTN_SPLITS");
+    return e ? atoi(e) : 0;
+  }();
+  const int qt = (t + BQ - 1) / BQ, ntk = (t + BKV - 1) / BKV;
+  if (forced > 0) return std::min(forced, ntk);
+  // Workgroups of one sequence = query tiles x heads x splits on 256 CUs (one
+  // workgroup each): pick the split count whose launch leaves the fewest
+  // slots idle, counting every round, with a small cost per extra split.
+  int best = 1;
+  double best_score = -1.0;
+  for (int s = 1; s <= std::min(8, ntk); ++s) {
+    const long w = (long)qt * HEADS * s;
+    const long rounds = (w + 255) / 256;
+    const double score = (double)w / (256.0 * rounds) - 0.06 * (s - 1);
+    if (score > best_score + 1e-9) {
+      best_score = score;
+      best = s;
+    }
+  }
+  return best;
+}
 
 void rel_attention(const AttnArgs& a, hipStream_t stream) {
   BARK_REQUIRE(a.ntiles > 0 && a.tiles, "rel_attention: no query tiles");
@@ -323,8 +417,14 @@ void rel_attention(const AttnArgs& a, hipStream_t stream) {
                                hipFuncAttributeMaxDynamicSharedMemorySize, sizeof(Smem)) == hipSuccess;
   }();
   BARK_REQUIRE(attr, "rel_attention: cannot reserve LDS");
+  BARK_REQUIRE(a.nmerges == 0 || (a.merges && a.part_o && a.part_ml), "rel_attention: missing partial buffers");
   hipLaunchKernelGGL(rel_attn_kernel, dim3(a.ntiles * HEADS), dim3(NT), sizeof(Smem), stream, a);
   BARK_HIP_CHECK(hipGetLastError());
+  if (a.nmerges > 0) {
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(a.nmerges * HEADS), dim3(256), 0, stream, a.part_o, a.part_ml,
+                       a.merges, a.out);
+    BARK_HIP_CHECK(hipGetLastError());
+  }
 }
 
 // scale * log2(e) applied to q+u and q+v by the qkv epilogue

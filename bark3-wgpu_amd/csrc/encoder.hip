@@ -205,6 +205,7 @@ struct BarkHip {
   // workspace
   DevBuf sub16, xn, hid, qu, qv, kh, vt, rk, ao, h, h2, glu, pooler, dump, bounds, tiles;
   DevBuf part;  // split-K partial sums of the residual linears
+  DevBuf merges, attn_po, attn_pml;  // attention key-range partials
   DevBuf y1, y2, y3, y4, mel, subf32;
 
   template <class T>
@@ -218,7 +219,7 @@ struct BarkHip {
 
   void ensure(DevBuf& b, size_t bytes) {
     if (bytes <= b.cap) return;
-    if (&b == &bounds || &b == &tiles) table_key.clear();
+    if (&b == &bounds || &b == &tiles || &b == &merges) table_key.clear();
     BARK_HIP_CHECK(hipDeviceSynchronize());  // any stream may still use the old buffer
     if (b.p) BARK_HIP_CHECK(hipFree(b.p));
     b.p = nullptr;
@@ -236,7 +237,8 @@ struct BarkHip {
     if (stream) (void)hipStreamSynchronize(stream);
     for (void* p : allocs) (void)hipFree(p);
     DevBuf* bufs[] = {&pos, &sub16, &xn, &hid, &qu, &qv, &kh, &vt, &rk, &ao, &h, &h2, &glu, &part,
-                      &pooler, &dump, &bounds, &tiles, &y1, &y2, &y3, &y4, &mel, &subf32};
+                      &pooler, &dump, &bounds, &tiles, &y1, &y2, &y3, &y4, &mel, &subf32,
+                      &merges, &attn_po, &attn_pml};
     for (DevBuf* b : bufs)
       if (b->p) (void)hipFree(b->p);
     if (stream) (void)hipStreamDestroy(stream);
@@ -503,8 +505,30 @@ struct BarkHip {
                      HIDDEN * 4);
     ensure(pooler, mp * PROJ * 4);
     ensure(bounds, mp * sizeof(int2));
-    ensure(tiles, (mp / 64 + pl.seqs.size()) * sizeof(int4));
+    std::vector<int4> tl, ml;
+    attention_tables(pl, tl, ml);
+    ensure(tiles, tl.size() * sizeof(int4));
+    ensure(merges, std::max<size_t>(ml.size(), 1) * sizeof(int4));
+    if (!ml.empty()) {
+      ensure(attn_po, tl.size() * HEADS * 128 * HDIM * 4);
+      ensure(attn_pml, tl.size() * HEADS * 128 * 2 * 4);
+    }
     ensure_pos(pl.tc);
+  }
+
+  // Attention work list: per sequence, query tiles x key-range splits, and a
+  // merge entry for every query tile with more than one split.
+  static void attention_tables(const Plan& pl, std::vector<int4>& tl, std::vector<int4>& ml) {
+    for (const auto& s : pl.seqs) {
+      const int ntk = (s.t + 63) / 64;
+      const int tps = (ntk + attention_splits(s.t) - 1) / attention_splits(s.t);  // key tiles per split
+      const int ns = (ntk + tps - 1) / tps;
+      for (int q0 = 0; q0 < s.t; q0 += 128) {
+        if (ns > 1) ml.push_back(make_int4((int)tl.size(), ns, s.start + q0, std::min(128, s.t - q0)));
+        for (int i = 0; i < ns; ++i)
+          tl.push_back(make_int4(s.start, s.t, q0, (i * tps) | (std::min(ntk, (i + 1) * tps) << 16)));
+      }
+    }
   }
 
   // Row bounds for the depthwise conv and query tiles for attention.
@@ -517,20 +541,23 @@ struct BarkHip {
     if (key == table_key) return;  // same packing as the previous call
     std::vector<int2> b(pl.mp);
     for (int r = 0; r < pl.mp; ++r) b[r] = make_int2(r, r + 1);
-    std::vector<int4> tl;
-    for (const auto& s : pl.seqs) {
+    for (const auto& s : pl.seqs)
       for (int r = s.start; r < s.start + s.t; ++r) b[r] = make_int2(s.start, s.start + s.t);
-      for (int q0 = 0; q0 < s.t; q0 += 128) tl.push_back(make_int4(s.start, s.t, q0, 0));
-    }
+    std::vector<int4> tl, ml;
+    attention_tables(pl, tl, ml);
     BARK_HIP_CHECK(hipMemcpyAsync(bounds.p, b.data(), b.size() * sizeof(int2),
                                   hipMemcpyHostToDevice, st));
     BARK_HIP_CHECK(hipMemcpyAsync(tiles.p, tl.data(), tl.size() * sizeof(int4),
                                   hipMemcpyHostToDevice, st));
+    if (!ml.empty())
+      BARK_HIP_CHECK(hipMemcpyAsync(merges.p, ml.data(), ml.size() * sizeof(int4),
+                                    hipMemcpyHostToDevice, st));
     ntiles = (int)tl.size();
+    nmerges = (int)ml.size();
     BARK_HIP_CHECK(hipStreamSynchronize(st));  // host vectors go out of scope
     table_key = key;
   }
-  int ntiles = 0;
+  int ntiles = 0, nmerges = 0;
 
   // Algorithmic bytes of a linear's weight operand.
   static double weight_bytes(const GemmWeight& w) {
@@ -661,7 +688,8 @@ struct BarkHip {
       gemm_op("qkv_heads", xnp, HIDDEN, mp, mr, L.qkv, Epi::Qkv, e, 2.0 * 4096, st);
       AttnArgs aa{qu.as<half>(), qv.as<half>(), kh.as<half>(), vt.as<half>(),
                   rk.as<half>() + (size_t)l * HEADS * pp * HDIM,
-                  ao.as<half>(), mp, pp, tc, tiles.as<int4>(), ntiles};
+                  ao.as<half>(), mp, pp, tc, tiles.as<int4>(), ntiles,
+                  attn_po.as<float>(), attn_pml.as<float>(), merges.as<int4>(), nmerges};
       prof.run("rel_attention", attn_flops, 2.0 * mr * HIDDEN * 5 + 2.0 * prows * HIDDEN, st,
                [&] { rel_attention(aa, st); });
       res = resid_op("attn_out_resid", ao.as<half>(), HIDDEN, mp, mr, L.o, 1.0f, st);

@@ -83,8 +83,12 @@ struct ResidIn {
 };
 
 // ----------------------------------------------------------- attention --
-// One entry per 128-query tile: {row of the sequence's first frame, sequence
-// length, first query of the tile (local), 0}.
+// One entry per (128-query tile, key range): {row of the sequence's first
+// frame, sequence length, first query of the tile (local), first key tile |
+// (end key tile << 16)} with 64-key tiles. An entry covering all keys writes
+// the output; otherwise it writes its unnormalised partial (o, max, sum) to
+// slot = entry index, and one merge entry {first slot, number of slots, first
+// output row, valid rows} combines the slots of a query tile in slot order.
 struct AttnArgs {
   const half *qu, *qv, *kh, *vt, *rk;
   half* out;       // (mp, 1024) heads-flat
@@ -93,7 +97,13 @@ struct AttnArgs {
   int tc;          // rk row j <-> relative position r = tc - 1 - j
   const int4* tiles;
   int ntiles;
+  float* part_o = nullptr;   // [slot][head][128 q][128 d]
+  float* part_ml = nullptr;  // [slot][head][128 q][2] (max, sum)
+  const int4* merges = nullptr;
+  int nmerges = 0;
 };
+// Key-range splits of one sequence's attention (a function of its length only).
+int attention_splits(int t);
 // q+u and q+v must be pre-multiplied by attention_q_scale() = log2(e)/sqrt(128)
 // (the Qkv epilogue does it when EpiArgs::scale is set to this value).
 void rel_attention(const AttnArgs& a, hipStream_t stream);
