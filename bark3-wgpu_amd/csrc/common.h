@@ -46,7 +46,6 @@ inline int round_up(int a, int b) { return ceil_div(a, b) * b; }
 __device__ inline half8 ld_half8(const half* p) { return *reinterpret_cast<const half8*>(p); }
 __device__ inline void st_half8(half* p, half8 v) { *reinterpret_cast<half8*>(p) = v; }
 
-__device__ inline float silu(float v) { return v / (1.0f + __expf(-v)); }
 
 // Butterfly reductions across the 64 lanes of a wave.
 __device__ inline float wave_sum(float v) {

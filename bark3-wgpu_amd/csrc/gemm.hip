@@ -581,6 +581,28 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
         if (r >= p.M) continue;
         ea.out_f32[(size_t)r * ea.ldo + c] = fast_sigmoid_mul(acc[i][0][v], acc[i][1][v]);
       }
+  } else if (EPI == (int)Epi::Qkv && nw >= 2048) {
+    // V^T[h][d][r]: a lane's four consecutive rows are contiguous, one 8-byte store
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int hd = nw - 2048 + 32 * j + l32;
+      half* vrow = ea.vt + (size_t)hd * ea.mp;  // (h*128 + d) == hd
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int r = m0 + i * 32 + 8 * g + 4 * lhi;
+          if (r + 3 < p.M) {
+            const half4 w4 = {(half)acc[i][j][4 * g], (half)acc[i][j][4 * g + 1], (half)acc[i][j][4 * g + 2],
+                              (half)acc[i][j][4 * g + 3]};
+            *reinterpret_cast<half4*>(vrow + r) = w4;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (r + e < p.M) vrow[r + e] = (half)acc[i][j][4 * g + e];
+          }
+        }
+    }
   } else {
 #pragma unroll
     for (int i = 0; i < FM; ++i)

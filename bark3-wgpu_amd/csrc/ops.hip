@@ -118,38 +118,79 @@ __global__ void __launch_bounds__(256) ln2_kernel(const float* x, const float* w
 // y[t,c] = sum_{i<9} x[t+i-4, c] * w[c,i] over frames inside the row's
 // sequence [start, end) (zero padding at the sequence edge, the length mask
 // of src/encoder/shader_sources.rs:344-376 / src/cpu/ops.rs:195-233), then
-// z = silu(y * a_c + b_c) with the folded BatchNorm. Each thread owns one
-// channel and 32 consecutive rows; the 40-row window is read once.
-constexpr int DW_ROWS = 32;
+// z = silu(y * a_c + b_c) with the folded BatchNorm; f32 multiply-adds in
+// ascending tap order (fused; the reference CPU rounds the product first,
+// a difference of an ulp per tap). A thread owns 4 consecutive channels
+// (float4 loads) and DW_ROWS consecutive rows, reading its (DW_ROWS + 8)-row
+// window once; a wave covers 256 channels, a workgroup 4 row groups. Row
+// groups whose windows lie inside their sequences skip the tap masks.
+constexpr int DW_ROWS = 4;
 
 __global__ void __launch_bounds__(256) dwconv_kernel(const float* g, const float* dw,
                                                      const float* bn_a, const float* bn_b,
                                                      const int2* bounds, half* out, int rows) {
-  const int c = blockIdx.y * 256 + threadIdx.x;
-  const int r0 = blockIdx.x * DW_ROWS;
-  float w[9];
+  const int c = (blockIdx.y * 64 + (threadIdx.x & 63)) * 4;
+  const int r0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (threadIdx.x >> 6)) * DW_ROWS);
+  if (r0 >= rows) return;
+  float w[4][9];
 #pragma unroll
-  for (int i = 0; i < 9; ++i) w[i] = dw[c * 9 + i];
-  const float a = bn_a[c], b = bn_b[c];
-  float win[DW_ROWS + 8];
+  for (int e = 0; e < 4; ++e)
+#pragma unroll
+    for (int i = 0; i < 9; ++i) w[e][i] = dw[(c + e) * 9 + i];
+  const floatx4 a = *reinterpret_cast<const floatx4*>(bn_a + c);
+  const floatx4 b = *reinterpret_cast<const floatx4*>(bn_b + c);
+  floatx4 win[DW_ROWS + 8];
 #pragma unroll
   for (int i = 0; i < DW_ROWS + 8; ++i) {
     const int r = r0 - 4 + i;
-    win[i] = (r >= 0 && r < rows) ? g[(size_t)r * HIDDEN + c] : 0.0f;
+    win[i] = (r >= 0 && r < rows) ? *reinterpret_cast<const floatx4*>(g + (size_t)r * HIDDEN + c)
+                                  : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  int2 be[DW_ROWS];
+  bool inside = r0 + DW_ROWS <= rows;
+#pragma unroll
+  for (int t = 0; t < DW_ROWS; ++t) {
+    be[t] = bounds[min(r0 + t, rows - 1)];  // wave-uniform
+    inside = inside && be[t].x <= r0 + t - 4 && r0 + t + 4 < be[t].y;
+  }
+  floatx4 y[DW_ROWS];
+  if (inside) {
+#pragma unroll
+    for (int t = 0; t < DW_ROWS; ++t) {
+      floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < 9; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = fmaf(win[t + i][e], w[e][i], acc[e]);
+      y[t] = acc;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < DW_ROWS; ++t) {
+      const int r = r0 + t;
+      floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < 9; ++i) {
+        const int rr = r + i - 4;
+        if (rr >= be[t].x && rr < be[t].y) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[e] = fmaf(win[t + i][e], w[e][i], acc[e]);
+        }
+      }
+      y[t] = acc;
+    }
   }
 #pragma unroll
   for (int t = 0; t < DW_ROWS; ++t) {
     const int r = r0 + t;
     if (r >= rows) break;
-    const int2 be = bounds[r];
-    float acc = 0.0f;
+    half4 z;
 #pragma unroll
-    for (int i = 0; i < 9; ++i) {
-      const int rr = r + i - 4;
-      if (rr >= be.x && rr < be.y) acc = __fadd_rn(acc, __fmul_rn(win[t + i], w[i]));
+    for (int e = 0; e < 4; ++e) {
+      const float v = fmaf(y[t][e], a[e], b[e]);
+      z[e] = (half)(v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)));
     }
-    const float y = __fadd_rn(__fmul_rn(acc, a), b);
-    out[(size_t)r * HIDDEN + c] = (half)silu(y);
+    *reinterpret_cast<half4*>(out + (size_t)r * HIDDEN + c) = z;
   }
 }
 
@@ -174,9 +215,9 @@ __global__ void copy_rows_kernel(const float* x, int ldx, float* y, int ldy, int
 // -------------------------------------------------------------- front end --
 // conv 1->256, 3x3, stride 2, pad 1, then ReLU (src/sub.rs:116-168). Output
 // layout is pixel-major with channels contiguous: out[(i*64 + j)*256 + c].
-// The sum is b + w0*x0 + ... + w8*x8 in tap order with separate multiply and
-// add roundings, as the reference AXPY does; rows i >= vlen are zeroed
-// (mask_time, src/sub.rs:288-300).
+// The sum is b + w0*x0 + ... + w8*x8 in tap order as fused multiply-adds (the
+// reference AXPY rounds each product first: an ulp per tap); rows i >= vlen
+// are zeroed (mask_time, src/sub.rs:288-300).
 constexpr int C1_PIX = 8;  // output pixels (along mel) per workgroup
 
 __global__ void __launch_bounds__(256) conv1_kernel(const float* mel, int frames,
@@ -202,7 +243,7 @@ __global__ void __launch_bounds__(256) conv1_kernel(const float* mel, int frames
     float acc = bias;
 #pragma unroll
     for (int t = 0; t < 9; ++t)
-      acc = __fadd_rn(acc, __fmul_rn(wr[t], patch[t / 3][2 * p + t % 3]));
+      acc = fmaf(wr[t], patch[t / 3][2 * p + t % 3], acc);
     acc = acc > 0.0f ? acc : 0.0f;
     if (masked) acc = 0.0f;
     out[((size_t)i * 64 + j0 + p) * SUB_CH + c] = (half)acc;
@@ -210,23 +251,31 @@ __global__ void __launch_bounds__(256) conv1_kernel(const float* mel, int frames
 }
 
 // depthwise 3x3 stride 2 pad 1 (src/sub.rs:174-203): s = b + sum w*x over the
-// in-range taps in (ki, kj) order; rows >= vlen zeroed.
-constexpr int DW2_PIX = 4;
+// in-range taps in (ki, kj) order (fused multiply-adds); rows >= vlen zeroed. A thread computes 8
+// consecutive channels of one output pixel with 16-byte loads; a workgroup
+// covers 8 pixels per pass (32 threads x 8 channels = 256 channels each).
+constexpr int DW2_PIX = 32;  // output pixels per workgroup
 
 __global__ void __launch_bounds__(256) sub_dw_kernel(const half* in, int t_in, int m_in,
                                                      const float* w, const float* b, half* out,
                                                      int t_out, int m_out, int vlen) {
-  const int c = threadIdx.x;
-  float wr[9];
+  const int c = (threadIdx.x & 31) * 8;
+  float wr[8][9];
 #pragma unroll
-  for (int t = 0; t < 9; ++t) wr[t] = w[c * 9 + t];
-  const float bias = b[c];
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int t = 0; t < 9; ++t) wr[e][t] = w[(c + e) * 9 + t];
+  float bias[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) bias[e] = b[c + e];
   const int npix = t_out * m_out;
-  for (int p = 0; p < DW2_PIX; ++p) {
+  for (int p = threadIdx.x >> 5; p < DW2_PIX; p += 8) {
     const int pix = blockIdx.x * DW2_PIX + p;
     if (pix >= npix) break;
     const int i = pix / m_out, j = pix % m_out;
-    float s = bias;
+    float s[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s[e] = bias[e];
 #pragma unroll
     for (int ki = 0; ki < 3; ++ki) {
       const int ii = 2 * i + ki - 1;
@@ -235,12 +284,15 @@ __global__ void __launch_bounds__(256) sub_dw_kernel(const half* in, int t_in, i
       for (int kj = 0; kj < 3; ++kj) {
         const int jj = 2 * j + kj - 1;
         if (jj < 0 || jj >= m_in) continue;
-        const float x = (float)in[((size_t)ii * m_in + jj) * SUB_CH + c];
-        s = __fadd_rn(s, __fmul_rn(wr[ki * 3 + kj], x));
+        const half8 x = ld_half8(in + ((size_t)ii * m_in + jj) * SUB_CH + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[e] = fmaf(wr[e][ki * 3 + kj], (float)x[e], s[e]);
       }
     }
-    if (i >= vlen) s = 0.0f;
-    out[(size_t)pix * SUB_CH + c] = (half)s;
+    half8 z;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) z[e] = (half)(i >= vlen ? 0.0f : s[e]);
+    st_half8(out + (size_t)pix * SUB_CH + c, z);
   }
 }
 
@@ -279,7 +331,7 @@ void apply_residual(float* x, int rows, const ResidIn& res, hipStream_t stream) 
 void dwconv_bn_silu(const float* g, const float* dw, const float* bn_a, const float* bn_b,
                     const int2* bounds, half* out, int rows, hipStream_t stream) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(dwconv_kernel, dim3(ceil_div(rows, DW_ROWS), HIDDEN / 256), dim3(256), 0,
+  hipLaunchKernelGGL(dwconv_kernel, dim3(ceil_div(rows, 4 * DW_ROWS), HIDDEN / 256), dim3(256), 0,
                      stream, g, dw, bn_a, bn_b, bounds, out, rows);
   BARK_HIP_CHECK(hipGetLastError());
 }
