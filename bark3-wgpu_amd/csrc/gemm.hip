@@ -28,6 +28,7 @@
 #include <cstdlib>
 #include <map>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 
 #include "kernels.h"
@@ -569,37 +570,120 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
     __syncthreads();
   }
 
+  // Epilogue. Lane (l32, lhi) holds, for MFMA block (i, j), column
+  // nw + 32j + l32 and rows m0 + 32i + 8g + 4lhi + b of acc[i][j][4g + b].
+  // Column-dependent work (bias, head/dim split, output base) is done once
+  // per column; row offsets are compile-time multiples of the row stride; a
+  // tile inside M skips the per-row bound checks.
   EpiArgs ea = p.ea;
   if constexpr (EPI == (int)Epi::StoreF32) ea.out_f32 += blockIdx.z * p.out_zstride;
+  const int mrow = m0 + 4 * lhi;  // row of acc element v = 0 of block i = 0
+  auto epilogue = [&](auto checked) {
+  constexpr bool CHK = decltype(checked)::value;
+  auto row_ok = [&](int rl) { return !CHK || mrow + rl < p.M; };  // rl = 32i + 8g + b
   if constexpr (EPI == (int)Epi::Glu) {
-    const int c = (nw >> 1) + l32;
+    float* base = ea.out_f32 + (size_t)mrow * ea.ldo + (nw >> 1) + l32;
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int r = m0 + i * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
-        if (r >= p.M) continue;
-        ea.out_f32[(size_t)r * ea.ldo + c] = fast_sigmoid_mul(acc[i][0][v], acc[i][1][v]);
+        const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
+        if (row_ok(rl)) base[(size_t)rl * ea.ldo] = fast_sigmoid_mul(acc[i][0][v], acc[i][1][v]);
       }
-  } else if (EPI == (int)Epi::Qkv && nw >= 2048) {
-    // V^T[h][d][r]: a lane's four consecutive rows are contiguous, one 8-byte store
+  } else if constexpr (EPI == (int)Epi::Qkv) {
+    const int region = __builtin_amdgcn_readfirstlane(nw >> 10);  // 0 q, 1 k, 2 v (wave-uniform)
+    if (region == 2) {
+      // V^T[h][d][r]: a lane's four consecutive rows are contiguous, one 8-byte store
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int hd = nw - 2048 + 32 * j + l32;  // h*128 + d
+        half* vrow = ea.vt + (size_t)hd * ea.mp + mrow;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int rl = 32 * i + 8 * g;
+            if (!CHK || mrow + rl + 3 < p.M) {
+              const half4 w4 = {(half)acc[i][j][4 * g], (half)acc[i][j][4 * g + 1],
+                                (half)acc[i][j][4 * g + 2], (half)acc[i][j][4 * g + 3]};
+              *reinterpret_cast<half4*>(vrow + rl) = w4;
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (mrow + rl + e < p.M) vrow[rl + e] = (half)acc[i][j][4 * g + e];
+            }
+          }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int hd = (nw & 1023) + 32 * j + l32, h = hd >> 7, d = hd & 127;
+        const size_t off = ((size_t)h * ea.mp + mrow) * HDIM + d;
+        if (region == 0) {
+          const float bu = ea.bu[hd], bv = ea.bv[hd];
+          half* pu = ea.qu + off;
+          half* pv = ea.qv + off;
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
+              if (row_ok(rl)) {
+                pu[rl * HDIM] = (half)((acc[i][j][v] + bu) * ea.scale);
+                pv[rl * HDIM] = (half)((acc[i][j][v] + bv) * ea.scale);
+              }
+            }
+        } else {
+          half* pk = ea.kh + off;
+#pragma unroll
+          for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
+              if (row_ok(rl)) pk[rl * HDIM] = (half)acc[i][j][v];
+            }
+        }
+      }
+    }
+  } else if constexpr (EPI == (int)Epi::RelK) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int hd = nw - 2048 + 32 * j + l32;
-      half* vrow = ea.vt + (size_t)hd * ea.mp;  // (h*128 + d) == hd
+      const int c = nw + 32 * j + l32, h = c >> 7, d = c & 127;
+      half* pr = ea.rk + ((size_t)h * ea.pp + mrow) * HDIM + d;
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int r = m0 + i * 32 + 8 * g + 4 * lhi;
-          if (r + 3 < p.M) {
-            const half4 w4 = {(half)acc[i][j][4 * g], (half)acc[i][j][4 * g + 1], (half)acc[i][j][4 * g + 2],
-                              (half)acc[i][j][4 * g + 3]};
-            *reinterpret_cast<half4*>(vrow + r) = w4;
-          } else {
+        for (int v = 0; v < 16; ++v) {
+          const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
+          if (row_ok(rl)) pr[rl * HDIM] = (half)acc[i][j][v];
+        }
+    }
+  } else if constexpr (EPI == (int)Epi::StoreF16 || EPI == (int)Epi::StoreBF16 || EPI == (int)Epi::Silu ||
+                       EPI == (int)Epi::BiasReluF16) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (r + e < p.M) vrow[r + e] = (half)acc[i][j][4 * g + e];
+    for (int j = 0; j < 2; ++j) {
+      const int c = nw + 32 * j + l32;
+      const float bc = ea.bias ? ea.bias[c] : 0.0f;
+      const size_t base = (size_t)mrow * ea.ldo + c;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
+          if (!row_ok(rl)) continue;
+          const size_t at = base + (size_t)rl * ea.ldo;
+          const float x = acc[i][j][v];
+          if constexpr (EPI == (int)Epi::StoreF16) {
+            ea.out_f16[at] = (half)(x + bc);
+          } else if constexpr (EPI == (int)Epi::StoreBF16) {
+            uint32_t u = __float_as_uint(x + bc);
+            u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite inputs)
+            reinterpret_cast<uint16_t*>(ea.out_f16)[at] = (uint16_t)(u >> 16);
+          } else if constexpr (EPI == (int)Epi::Silu) {
+            ea.out_f16[at] = (half)fast_sigmoid_mul(x, x);
+          } else {
+            const float y = x + bc;
+            ea.out_f16[at] = (half)(y > 0.0f ? y : 0.0f);
           }
         }
     }
@@ -614,6 +698,12 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
           if (r < p.M) store_one<EPI>(ea, r, nw + 32 * j + l32, acc[i][j][v]);
         }
   }
+  };
+  // a tile inside M skips every per-row check (the f32 store, the split-K
+  // partial, measured faster with the checks kept: one code path)
+  if constexpr (EPI == (int)Epi::StoreF32 || EPI == (int)Epi::FlattenReluF16) epilogue(std::integral_constant<bool, true>());
+  else if (m0 + BM <= p.M) epilogue(std::integral_constant<bool, false>());
+  else epilogue(std::integral_constant<bool, true>());
 }
 
 // out[r][c] = sum_s part[s][r][c] (s ascending), stored as f32 / f16 / bf16
