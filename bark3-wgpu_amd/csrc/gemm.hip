@@ -103,6 +103,15 @@ __device__ inline uint4 expand8(uint32_t w, const RowLut& t) {
   }
 }
 
+// f32 -> f16 after materialising the f32 value: the compiler may otherwise
+// fuse a multiply with the conversion (one rounding) in some epilogue
+// instantiations and not in others, which would make a row's f16 output
+// depend on the tile it falls in.
+__device__ inline half to_f16(float x) {
+  asm volatile("" : "+v"(x));
+  return (half)x;
+}
+
 __device__ inline float fast_sigmoid_mul(float a, float g) {
   return a * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }
@@ -114,14 +123,14 @@ __device__ inline void store_one(const EpiArgs& ea, int r, int c, float v) {
     ea.out_f32[(size_t)r * ea.ldo + c] = v;
   } else if constexpr (EPI == (int)Epi::StoreF16) {
     if (ea.bias) v += ea.bias[c];
-    ea.out_f16[(size_t)r * ea.ldo + c] = (half)v;
+    ea.out_f16[(size_t)r * ea.ldo + c] = to_f16(v);
   } else if constexpr (EPI == (int)Epi::StoreBF16) {
     if (ea.bias) v += ea.bias[c];
     uint32_t u = __float_as_uint(v);
     u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite inputs)
     reinterpret_cast<uint16_t*>(ea.out_f16)[(size_t)r * ea.ldo + c] = (uint16_t)(u >> 16);
   } else if constexpr (EPI == (int)Epi::Silu) {
-    ea.out_f16[(size_t)r * ea.ldo + c] = (half)fast_sigmoid_mul(v, v);
+    ea.out_f16[(size_t)r * ea.ldo + c] = to_f16(fast_sigmoid_mul(v, v));
   } else if constexpr (EPI == (int)Epi::Resid) {
     float* p = ea.out_f32 + (size_t)r * ea.ldo + c;
     *p = *p + ea.scale * v;
@@ -132,23 +141,23 @@ __device__ inline void store_one(const EpiArgs& ea, int r, int c, float v) {
     const int which = c >> 10, hd = c & 1023, h = hd >> 7, d = hd & 127;
     const size_t hr = ((size_t)h * ea.mp + r) * HDIM + d;
     if (which == 0) {
-      ea.qu[hr] = (half)((v + ea.bu[hd]) * ea.scale);
-      ea.qv[hr] = (half)((v + ea.bv[hd]) * ea.scale);
+      ea.qu[hr] = to_f16((v + ea.bu[hd]) * ea.scale);
+      ea.qv[hr] = to_f16((v + ea.bv[hd]) * ea.scale);
     } else if (which == 1) {
-      ea.kh[hr] = (half)v;
+      ea.kh[hr] = to_f16(v);
     } else {
-      ea.vt[((size_t)h * HDIM + d) * ea.mp + r] = (half)v;
+      ea.vt[((size_t)h * HDIM + d) * ea.mp + r] = to_f16(v);
     }
   } else if constexpr (EPI == (int)Epi::RelK) {
     const int h = c >> 7, d = c & 127;
-    ea.rk[((size_t)h * ea.pp + r) * HDIM + d] = (half)v;
+    ea.rk[((size_t)h * ea.pp + r) * HDIM + d] = to_f16(v);
   } else if constexpr (EPI == (int)Epi::BiasReluF16) {
     v += ea.bias[c];
-    ea.out_f16[(size_t)r * ea.ldo + c] = (half)(v > 0.0f ? v : 0.0f);
+    ea.out_f16[(size_t)r * ea.ldo + c] = to_f16(v > 0.0f ? v : 0.0f);
   } else if constexpr (EPI == (int)Epi::FlattenReluF16) {
     v += ea.bias[c];
     const int t = r >> 4, m = r & 15;
-    ea.out_f16[(size_t)t * ea.ldo + c * 16 + m] = (half)(v > 0.0f ? v : 0.0f);
+    ea.out_f16[(size_t)t * ea.ldo + c * 16 + m] = to_f16(v > 0.0f ? v : 0.0f);
   }
 }
 
@@ -604,13 +613,13 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
           for (int g = 0; g < 4; ++g) {
             const int rl = 32 * i + 8 * g;
             if (!CHK || mrow + rl + 3 < p.M) {
-              const half4 w4 = {(half)acc[i][j][4 * g], (half)acc[i][j][4 * g + 1],
-                                (half)acc[i][j][4 * g + 2], (half)acc[i][j][4 * g + 3]};
+              const half4 w4 = {to_f16(acc[i][j][4 * g]), to_f16(acc[i][j][4 * g + 1]),
+                                to_f16(acc[i][j][4 * g + 2]), to_f16(acc[i][j][4 * g + 3])};
               *reinterpret_cast<half4*>(vrow + rl) = w4;
             } else {
 #pragma unroll
               for (int e = 0; e < 4; ++e)
-                if (mrow + rl + e < p.M) vrow[rl + e] = (half)acc[i][j][4 * g + e];
+                if (mrow + rl + e < p.M) vrow[rl + e] = to_f16(acc[i][j][4 * g + e]);
             }
           }
       }
@@ -629,8 +638,8 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
             for (int v = 0; v < 16; ++v) {
               const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
               if (row_ok(rl)) {
-                pu[rl * HDIM] = (half)((acc[i][j][v] + bu) * ea.scale);
-                pv[rl * HDIM] = (half)((acc[i][j][v] + bv) * ea.scale);
+                pu[rl * HDIM] = to_f16((acc[i][j][v] + bu) * ea.scale);
+                pv[rl * HDIM] = to_f16((acc[i][j][v] + bv) * ea.scale);
               }
             }
         } else {
@@ -640,7 +649,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
               const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
-              if (row_ok(rl)) pk[rl * HDIM] = (half)acc[i][j][v];
+              if (row_ok(rl)) pk[rl * HDIM] = to_f16(acc[i][j][v]);
             }
         }
       }
@@ -655,7 +664,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
-          if (row_ok(rl)) pr[rl * HDIM] = (half)acc[i][j][v];
+          if (row_ok(rl)) pr[rl * HDIM] = to_f16(acc[i][j][v]);
         }
     }
   } else if constexpr (EPI == (int)Epi::StoreF16 || EPI == (int)Epi::StoreBF16 || EPI == (int)Epi::Silu ||
@@ -674,16 +683,16 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
           const size_t at = base + (size_t)rl * ea.ldo;
           const float x = acc[i][j][v];
           if constexpr (EPI == (int)Epi::StoreF16) {
-            ea.out_f16[at] = (half)(x + bc);
+            ea.out_f16[at] = to_f16(x + bc);
           } else if constexpr (EPI == (int)Epi::StoreBF16) {
             uint32_t u = __float_as_uint(x + bc);
             u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite inputs)
             reinterpret_cast<uint16_t*>(ea.out_f16)[at] = (uint16_t)(u >> 16);
           } else if constexpr (EPI == (int)Epi::Silu) {
-            ea.out_f16[at] = (half)fast_sigmoid_mul(x, x);
+            ea.out_f16[at] = to_f16(fast_sigmoid_mul(x, x));
           } else {
             const float y = x + bc;
-            ea.out_f16[at] = (half)(y > 0.0f ? y : 0.0f);
+            ea.out_f16[at] = to_f16(y > 0.0f ? y : 0.0f);
           }
         }
     }
