@@ -692,6 +692,9 @@ struct BarkHip {
                   attn_po.as<float>(), attn_pml.as<float>(), merges.as<int4>(), nmerges};
       prof.run("rel_attention", attn_flops, 2.0 * mr * HIDDEN * 5 + 2.0 * prows * HIDDEN, st,
                [&] { rel_attention(aa, st); });
+      if (nmerges)  // partial (o, max, sum) of every split query tile -> heads-flat f16
+        prof.run("attn_merge", 0, (double)ntiles * HEADS * 128 * (HDIM + 2) * 4 + 2.0 * mr * HIDDEN, st,
+                 [&] { rel_attention_merge(aa, st); });
       res = resid_op("attn_out_resid", ao.as<half>(), HIDDEN, mp, mr, L.o, 1.0f, st);
       // ---- conv module
       prof.run("layernorm_resid", 0, ln_bytes + 4.0 * (res.splits + 1) * mr * HIDDEN, st,

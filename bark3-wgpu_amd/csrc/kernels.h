@@ -106,7 +106,10 @@ struct AttnArgs {
 int attention_splits(int t);
 // q+u and q+v must be pre-multiplied by attention_q_scale() = log2(e)/sqrt(128)
 // (the Qkv epilogue does it when EpiArgs::scale is set to this value).
+// rel_attention writes the complete query tiles and the partials of split
+// ones; rel_attention_merge (a no-op without splits) then writes the rest.
 void rel_attention(const AttnArgs& a, hipStream_t stream);
+void rel_attention_merge(const AttnArgs& a, hipStream_t stream);
 float attention_q_scale();
 
 // ----------------------------------------------------------------- ops --

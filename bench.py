@@ -173,6 +173,26 @@ def cpu_baseline(synth, blocks: int):
     return {"value": AUDIO_S / total, "unit": "audio s/s", "cores": threads, "kind": "port", "sample": sample}
 
 
+def traffic_workload(pkg, synth, torch) -> None:
+    """What the HBM-traffic counter passes profile (rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE -- python3 bench.py --traffic-workload): a 512 MiB device copy
+    whose bytes calibrate the counters, then two 1-block encodes at T=2207 (the
+    per-layer launches of the config-3 step)."""
+    a = torch.empty(128 << 20, dtype=torch.float32, device="cuda")
+    a.fill_(1.0)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    b.copy_(a)
+    torch.cuda.synchronize()
+    src = synth.SynthCheckpoint(seed=0, n_layers=1, style="baseline", lowbit=True)
+    with pkg.HipEncoder.load_with(src, device=0, n_layers=1, front_end=False) as enc:
+        sub = np.random.default_rng(0).standard_normal((2207, 4096), dtype=np.float32)
+        enc.encode(sub, 2207)
+        enc.encode(sub, 2207)
+    torch.cuda.synchronize()
+    log("[bench] traffic workload done")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -181,6 +201,8 @@ def main() -> int:
     ap.add_argument("--cpu-blocks", type=int, default=24)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
+    ap.add_argument("--traffic-workload", action="store_true",
+                    help="run only the workload of the HBM-traffic counter passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -194,6 +216,10 @@ def main() -> int:
     if not torch.cuda.is_available() or pkg.lib().bark_hip_device_count() < 1:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
+
+    if args.traffic_workload:
+        traffic_workload(pkg, synth, torch)
+        return 0
 
     dt, T, prof, dom, d = bench_encoder(pkg, synth, torch, args.steps, args.warmup)
     # roofline of the dominant kernel from its launches inside the timed region
