@@ -136,46 +136,48 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
   }
 
   // The next key tile into registers. K rows and V^T columns past T stay inside
-  // the sequence's 64-row-aligned slot of the packed buffers; they read as
-  // zero (keys past T are also masked out of the softmax).
+  // the sequence's 64-row-aligned slot of the packed buffers; they are zeroed
+  // when staged (keys past T are also masked out of the softmax). The masks
+  // are applied at staging, not here, so the loads stay in flight across the
+  // current tile's work.
   uint4 kr[K_CH], vr[V_CH], rr[R_NEW];
   auto fetch = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < K_CH; ++i) {
-      const int k = k0 + row16 + 16 * i;
-      const uint4 v = *reinterpret_cast<const uint4*>(kbase + (size_t)k * HDIM + col16);
-      kr[i] = keep_if(k < T, v);
-    }
+    for (int i = 0; i < K_CH; ++i)
+      kr[i] = *reinterpret_cast<const uint4*>(kbase + (size_t)(k0 + row16 + 16 * i) * HDIM + col16);
+#pragma unroll
+    for (int i = 0; i < V_CH; ++i)
+      vr[i] = *reinterpret_cast<const uint4*>(vbase + (size_t)(v_d + 32 * i) * a.mp + k0 + v_kc);
+    const int jn = jg00 + k0 + 128;  // first new band row of the tile at k0
+#pragma unroll
+    for (int i = 0; i < R_NEW; ++i)
+      rr[i] = *reinterpret_cast<const uint4*>(rbase + (size_t)min(max(jn + row16 + 16 * i, 0), prows - 1) * HDIM + col16);
+  };
+  auto stage = [&](int k0, int t) {
+#pragma unroll
+    for (int i = 0; i < K_CH; ++i)
+      *reinterpret_cast<uint4*>(&sm.K[(row16 + 16 * i) * KLD + col16]) = keep_if(k0 + row16 + 16 * i < T, kr[i]);
 #pragma unroll
     for (int i = 0; i < V_CH; ++i) {
-      const int k = k0 + v_kc;
-      uint4 v = *reinterpret_cast<const uint4*>(vbase + (size_t)(v_d + 32 * i) * a.mp + k);
       // keys k .. k+7 of this chunk: zero the ones past the sequence end
-      const int nvalid = T - k;  // <= 0: none, >= 8: all
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      const int nvalid = T - (k0 + v_kc);  // <= 0: none, >= 8: all
+      const uint32_t w[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
       uint32_t o4[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t lo = 2 * e < nvalid ? 0x0000ffffu : 0u, hi = 2 * e + 1 < nvalid ? 0xffff0000u : 0u;
         o4[e] = w[e] & (lo | hi);
       }
-      vr[i] = uint4{o4[0], o4[1], o4[2], o4[3]};
+      *reinterpret_cast<uint4*>(&sm.V[(v_d + 32 * i) * VLD + v_kc]) = uint4{o4[0], o4[1], o4[2], o4[3]};
     }
-    const int jn = jg00 + k0 + 128;  // first new band row of the tile at k0
-#pragma unroll
-    for (int i = 0; i < R_NEW; ++i) rr[i] = r_load(jn + row16 + 16 * i);
-  };
-  auto stage = [&](int t) {
-#pragma unroll
-    for (int i = 0; i < K_CH; ++i) *reinterpret_cast<uint4*>(&sm.K[(row16 + 16 * i) * KLD + col16]) = kr[i];
-#pragma unroll
-    for (int i = 0; i < V_CH; ++i) *reinterpret_cast<uint4*>(&sm.V[(v_d + 32 * i) * VLD + v_kc]) = vr[i];
     if (t > 0) {  // new band rows 128..191 of tile t -> ring blocks (4,5) + 2t
+      const int jn = jg00 + k0 + 128;
 #pragma unroll
       for (int i = 0; i < R_NEW; ++i) {
         const int r = 128 + row16 + 16 * i;
         const int prow = (((r >> 5) + 2 * t) % 6) * 32 + (r & 31);
-        *reinterpret_cast<uint4*>(&sm.R[prow * KLD + col16]) = rr[i];
+        const int j = jn + row16 + 16 * i;
+        *reinterpret_cast<uint4*>(&sm.R[prow * KLD + col16]) = keep_if(j >= 0 && j < prows, rr[i]);
       }
     }
   };
@@ -184,7 +186,7 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
   fetch(k_begin);
   int t = 0;
   for (int k0 = k_begin; k0 < k_end; k0 += BKV, ++t) {
-    stage(t);
+    stage(k0, t);
     __syncthreads();
     if (k0 + BKV < k_end) fetch(k0 + BKV);
 
