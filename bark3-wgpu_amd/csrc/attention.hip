@@ -52,11 +52,23 @@ constexpr int V_CH = HDIM * BKV / 8 / NT;
 constexpr int R_NEW = 64 * HDIM / 8 / NT;   // new band rows per tile
 constexpr int R_CH = BAND * HDIM / 8 / NT;
 
-// v if ok else zero, per component (a select of whole uint4 objects makes the
-// compiler pick between two stack slots instead of registers)
-__device__ inline uint4 keep_if(bool ok, const uint4& v) {
-  const uint32_t m = ok ? 0xffffffffu : 0u;
-  return uint4{v.x & m, v.y & m, v.z & m, v.w & m};
+// Register-class pins (empty asm): keep a value in the accumulation registers
+// (AGPRs: the output accumulators, which MFMA updates in place) or in the
+// vector registers (values the VALU works on). Without them the allocator
+// copies the 64 output accumulators between the two files every key tile. (A
+// pin makes the value ready at that point, so it never goes on a load.)
+template <typename T>
+__device__ inline void pin_acc(T& x) {
+  asm volatile("" : "+a"(x));
+}
+template <typename T>
+__device__ inline void pin_vgpr(T& x) {
+  asm volatile("" : "+v"(x));
+}
+
+// 16 bytes at base + byte offset off (a uniform base and a 32-bit lane offset)
+__device__ inline uint4 ld_u4(const half* base, uint32_t off) {
+  return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + off);
 }
 
 struct Smem {
@@ -79,7 +91,8 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
   const int start = tile.x, T = tile.y, q0 = tile.z;
   const int k_begin = (tile.w & 0xffff) * BKV, k_end = min(T, (tile.w >> 16) * BKV);
   const bool complete = k_begin == 0 && k_end == T;
-  const int tid = threadIdx.x, lane = tid & 63, qg = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int qg = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (uniform)
   const int l32 = lane & 31, lhi = lane >> 5;
   const int q_lane = q0 + 32 * qg + l32;
   const int prows = 2 * a.tc - 1;
@@ -124,15 +137,11 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
   // Each tile only fetches its last 64 rows (the first 128 are the previous
   // tile's last 128). The band of the tile at key k0 starts at row jg00 + k0.
   const int jg00 = a.tc - 1 - (q0 + BQ - 1);
-  // relK row j clamped into the head's block (rows outside [0, prows) read as zero)
-  auto r_load = [&](int j) {
-    const uint4 v = *reinterpret_cast<const uint4*>(rbase + (size_t)min(max(j, 0), prows - 1) * HDIM + col16);
-    return keep_if(j >= 0 && j < prows, v);
-  };
 #pragma unroll 4
-  for (int i = 0; i < R_CH; ++i) {  // first tile: all 192 rows
+  for (int i = 0; i < R_CH; ++i) {  // first tile: all 192 rows (row index clamped into the block)
     const int row = row16 + 16 * i;
-    *reinterpret_cast<uint4*>(&sm.R[row * KLD + col16]) = r_load(jg00 + k_begin + row);
+    *reinterpret_cast<uint4*>(&sm.R[row * KLD + col16]) =
+        *reinterpret_cast<const uint4*>(rbase + (size_t)min(max(jg00 + k_begin + row, 0), prows - 1) * HDIM + col16);
   }
 
   // The next key tile into registers. K rows and V^T columns past T stay inside
@@ -141,44 +150,51 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
   // are applied at staging, not here, so the loads stay in flight across the
   // current tile's work.
   uint4 kr[K_CH], vr[V_CH], rr[R_NEW];
+  // Load n (0 .. 11) of the key tile at k0: K rows, V^T columns, new band rows.
+  // Uniform tile bases (readfirstlane keeps the compiler from turning the
+  // addresses into per-load 64-bit pointer recurrences) plus 32-bit lane byte
+  // offsets; a head's block is < 2^31 elements (checked on the host).
+  auto fetch_one = [&](int k0_, int n) {
+    const int k0 = __builtin_amdgcn_readfirstlane(k0_);
+    if (n < K_CH) {
+      kr[n] = ld_u4(kbase + (size_t)k0 * HDIM, (uint32_t)((row16 + 16 * n) * HDIM + col16) * 2u);
+    } else if (n < K_CH + V_CH) {
+      const int i = n - K_CH;
+      vr[i] = ld_u4(vbase + k0, (uint32_t)((v_d + 32 * i) * a.mp + v_kc) * 2u);
+    } else {
+      const int i = n - K_CH - V_CH;
+      const int jn = jg00 + k0 + 128;  // first new band row of the tile at k0
+      rr[i] = ld_u4(rbase, (uint32_t)(min(max(jn + row16 + 16 * i, 0), prows - 1) * HDIM + col16) * 2u);
+    }
+  };
+  constexpr int N_FETCH = K_CH + V_CH + R_NEW;
   auto fetch = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < K_CH; ++i)
-      kr[i] = *reinterpret_cast<const uint4*>(kbase + (size_t)(k0 + row16 + 16 * i) * HDIM + col16);
-#pragma unroll
-    for (int i = 0; i < V_CH; ++i)
-      vr[i] = *reinterpret_cast<const uint4*>(vbase + (size_t)(v_d + 32 * i) * a.mp + k0 + v_kc);
-    const int jn = jg00 + k0 + 128;  // first new band row of the tile at k0
-#pragma unroll
-    for (int i = 0; i < R_NEW; ++i)
-      rr[i] = *reinterpret_cast<const uint4*>(rbase + (size_t)min(max(jn + row16 + 16 * i, 0), prows - 1) * HDIM + col16);
+    for (int n = 0; n < N_FETCH; ++n) fetch_one(k0, n);
   };
+  // Staging needs no masks on K or relK: scores of keys >= T are replaced by
+  // -inf in the softmax whatever K holds, and band rows outside [0, prows)
+  // (clamped loads of valid rows) only meet (query, key) pairs with a query or
+  // key past the sequence end. V^T columns of keys >= T are zeroed: their P is
+  // 0, but 0 * (stale data) need not be 0.
   auto stage = [&](int k0, int t) {
 #pragma unroll
-    for (int i = 0; i < K_CH; ++i)
-      *reinterpret_cast<uint4*>(&sm.K[(row16 + 16 * i) * KLD + col16]) = keep_if(k0 + row16 + 16 * i < T, kr[i]);
+    for (int i = 0; i < K_CH; ++i) *reinterpret_cast<uint4*>(&sm.K[(row16 + 16 * i) * KLD + col16]) = kr[i];
 #pragma unroll
-    for (int i = 0; i < V_CH; ++i) {
-      // keys k .. k+7 of this chunk: zero the ones past the sequence end
-      const int nvalid = T - (k0 + v_kc);  // <= 0: none, >= 8: all
-      const uint32_t w[4] = {vr[i].x, vr[i].y, vr[i].z, vr[i].w};
-      uint32_t o4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t lo = 2 * e < nvalid ? 0x0000ffffu : 0u, hi = 2 * e + 1 < nvalid ? 0xffff0000u : 0u;
-        o4[e] = w[e] & (lo | hi);
-      }
-      *reinterpret_cast<uint4*>(&sm.V[(v_d + 32 * i) * VLD + v_kc]) = uint4{o4[0], o4[1], o4[2], o4[3]};
-    }
+    for (int i = 0; i < V_CH; ++i) *reinterpret_cast<uint4*>(&sm.V[(v_d + 32 * i) * VLD + v_kc]) = vr[i];
     if (t > 0) {  // new band rows 128..191 of tile t -> ring blocks (4,5) + 2t
-      const int jn = jg00 + k0 + 128;
 #pragma unroll
       for (int i = 0; i < R_NEW; ++i) {
         const int r = 128 + row16 + 16 * i;
-        const int prow = (((r >> 5) + 2 * t) % 6) * 32 + (r & 31);
-        const int j = jn + row16 + 16 * i;
-        *reinterpret_cast<uint4*>(&sm.R[prow * KLD + col16]) = keep_if(j >= 0 && j < prows, rr[i]);
+        *reinterpret_cast<uint4*>(&sm.R[((((r >> 5) + 2 * t) % 6) * 32 + (r & 31)) * KLD + col16]) = rr[i];
       }
+    }
+    if (k0 + BKV > T) {  // the sequence's last tile (uniform branch)
+      const int e0 = max(T - (k0 + v_kc), 0);  // valid keys of this thread's 8-key chunk
+#pragma unroll
+      for (int i = 0; i < V_CH; ++i)
+#pragma nounroll
+        for (int e = e0; e < 8; ++e) sm.V[(v_d + 32 * i) * VLD + v_kc + e] = (half)0.0f;
     }
   };
 
@@ -186,9 +202,15 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
   fetch(k_begin);
   int t = 0;
   for (int k0 = k_begin; k0 < k_end; k0 += BKV, ++t) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db) pin_acc(o[db]);
     stage(k0, t);
     __syncthreads();
-    if (k0 + BKV < k_end) fetch(k0 + BKV);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) pin_acc(o[db]);
+    // The next tile's loads are issued two per step of the MFMA loop below
+    // (the last tile re-reads its own valid addresses, so no branch is needed).
+    const int k_next = k0 + BKV < k_end ? k0 + BKV : k0;
 
     // ---- content scores S^T (two 32-key blocks x 32 queries) and the position
     // band relK[j] . Qv^T over the wave's 96 band rows: five independent MFMA
@@ -198,18 +220,31 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
     for (int v = 0; v < 16; ++v) s0[v] = s1[v] = bd0[v] = bd1[v] = bd2[v] = 0.0f;
     const int pb = (rb0 >> 5) + 2 * t;
     const int pb0 = pb % 6, pb1 = (pb + 1) % 6, pb2 = (pb + 2) % 6;  // ring blocks
+    // Fragment reads run one 16-dim step ahead of the MFMAs (two register
+    // sets); scheduling barriers keep the compiler from pulling them back
+    // next to their MFMAs.
+    half8 fr[2][5];
+    auto frag_load = [&](int st, half8* f) {
+      f[0] = ld_half8(&sm.K[l32 * KLD + 16 * st + 8 * lhi]);
+      f[1] = ld_half8(&sm.K[(32 + l32) * KLD + 16 * st + 8 * lhi]);
+      f[2] = ld_half8(&sm.R[(pb0 * 32 + l32) * KLD + 16 * st + 8 * lhi]);
+      f[3] = ld_half8(&sm.R[(pb1 * 32 + l32) * KLD + 16 * st + 8 * lhi]);
+      f[4] = ld_half8(&sm.R[(pb2 * 32 + l32) * KLD + 16 * st + 8 * lhi]);
+    };
+    frag_load(0, fr[0]);
 #pragma unroll
     for (int st = 0; st < 8; ++st) {
-      const half8 k0f = ld_half8(&sm.K[l32 * KLD + 16 * st + 8 * lhi]);
-      const half8 k1f = ld_half8(&sm.K[(32 + l32) * KLD + 16 * st + 8 * lhi]);
-      const half8 r0 = ld_half8(&sm.R[(pb0 * 32 + l32) * KLD + 16 * st + 8 * lhi]);
-      const half8 r1 = ld_half8(&sm.R[(pb1 * 32 + l32) * KLD + 16 * st + 8 * lhi]);
-      const half8 r2 = ld_half8(&sm.R[(pb2 * 32 + l32) * KLD + 16 * st + 8 * lhi]);
-      s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0f, quf[st], s0, 0, 0, 0);
-      bd0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(r0, qvf[st], bd0, 0, 0, 0);
-      s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1f, quf[st], s1, 0, 0, 0);
-      bd1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(r1, qvf[st], bd1, 0, 0, 0);
-      bd2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(r2, qvf[st], bd2, 0, 0, 0);
+      if (st < 7) frag_load(st + 1, fr[(st + 1) & 1]);
+      if (2 * st < N_FETCH) fetch_one(k_next, 2 * st);
+      if (2 * st + 1 < N_FETCH) fetch_one(k_next, 2 * st + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const half8* f = fr[st & 1];
+      s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[0], quf[st], s0, 0, 0, 0);
+      bd0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[2], qvf[st], bd0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[1], quf[st], s1, 0, 0, 0);
+      bd1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[3], qvf[st], bd1, 0, 0, 0);
+      bd2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[4], qvf[st], bd2, 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -225,18 +260,28 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // ---- rel-shift (diagonal read), mask, online softmax (log2 domain)
-    const bool tail = k0 + BKV > T;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) pin_acc(o[db]);
+    // The row max is taken right after the sums in the same block, where the
+    // compiler can see its inputs are arithmetic results and needs no
+    // NaN-quieting; the sequence's last tile masks keys >= T and redoes it.
     float mt = -INFINITY;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int kk = 8 * (v >> 2) + 4 * lhi + (v & 3);  // key within a 32-key block
-      float x0 = s0[v] + ps[l32 * PLD + kk + 31 - l32];
-      float x1 = s1[v] + ps[l32 * PLD + 32 + kk + 31 - l32];
-      if (tail && k0 + kk >= T) x0 = -INFINITY;
-      if (tail && k0 + 32 + kk >= T) x1 = -INFINITY;
-      s0[v] = x0;
-      s1[v] = x1;
-      mt = fmaxf(mt, fmaxf(x0, x1));
+      s0[v] += ps[l32 * PLD + kk + 31 - l32];
+      s1[v] += ps[l32 * PLD + 32 + kk + 31 - l32];
+      mt = fmaxf(mt, fmaxf(s0[v], s1[v]));
+    }
+    if (k0 + BKV > T) {  // uniform branch
+      mt = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int kk = 8 * (v >> 2) + 4 * lhi + (v & 3);
+        if (k0 + kk >= T) s0[v] = -INFINITY;
+        if (k0 + 32 + kk >= T) s1[v] = -INFINITY;
+        mt = fmaxf(mt, fmaxf(s0[v], s1[v]));
+      }
     }
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     // Lazy rescaling: exp2 is taken against a reference max m_run that is only
@@ -248,9 +293,14 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
       const float corr = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= corr;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+      for (int db = 0; db < 4; ++db) {
+        floatx16 x = o[db];
+        pin_vgpr(x);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) o[db][v] *= corr;
+        for (int v = 0; v < 16; ++v) x[v] *= corr;
+        pin_acc(x);
+        o[db] = x;
+      }
       m_run = m_new;
     }
     const float m_use = m_run == -INFINITY ? 0.0f : m_run;  // no valid key yet
@@ -283,6 +333,8 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, o[db], 0, 0, 0);
         }
       }
+#pragma unroll
+    for (int db = 0; db < 4; ++db) pin_acc(o[db]);
     __syncthreads();
   }
 
@@ -319,40 +371,34 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
 
 // Combines the key-range partials of one (query tile, head): with weights
 // w_s = 2^(m_s - max_s m_s), out = sum_s w_s o_s / sum_s w_s l_s, slots in
-// order. Thread t handles query t/2, dims 64*(t&1) .. +63.
+// order. A workgroup covers 8 queries of one (merge entry, head); thread t
+// handles query 8 * (group % 16) + t / 32, dims 4 * (t % 32) .. +3, so a launch
+// has 16 workgroups per (query tile, head) and each thread streams one float4
+// per slot.
+constexpr int MERGE_Q = 8;
 __global__ void __launch_bounds__(256) attn_merge_kernel(const float* part_o, const float* part_ml,
                                                          const int4* merges, half* out) {
   const int h = blockIdx.x % HEADS;
-  const int4 mg = merges[blockIdx.x / HEADS];
-  const int q = threadIdx.x >> 1, d0 = (threadIdx.x & 1) * 64;
+  const int rest = blockIdx.x / HEADS;
+  const int4 mg = merges[rest / (BQ / MERGE_Q)];
+  const int q = (rest % (BQ / MERGE_Q)) * MERGE_Q + (threadIdx.x >> 5);
+  const int d = (threadIdx.x & 31) * 4;
   if (q >= mg.w) return;
   float m = -INFINITY;
-  for (int s = 0; s < mg.y; ++s)
-    m = fmaxf(m, part_ml[(((size_t)(mg.x + s) * HEADS + h) * BQ + q) * 2]);
-  float o[64];
-#pragma unroll
-  for (int i = 0; i < 64; ++i) o[i] = 0.0f;
+  for (int s = 0; s < mg.y; ++s) m = fmaxf(m, part_ml[(((size_t)(mg.x + s) * HEADS + h) * BQ + q) * 2]);
+  floatx4 o = {0.0f, 0.0f, 0.0f, 0.0f};
   float l = 0.0f;
   for (int s = 0; s < mg.y; ++s) {
     const size_t sh = ((size_t)(mg.x + s) * HEADS + h) * BQ + q;
     const float w = __builtin_amdgcn_exp2f(part_ml[sh * 2] - m);
     l += w * part_ml[sh * 2 + 1];
-    const floatx4* src = reinterpret_cast<const floatx4*>(part_o + sh * HDIM + d0);
+    const floatx4 v = *reinterpret_cast<const floatx4*>(part_o + sh * HDIM + d);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const floatx4 v = src[i];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[4 * i + e] += w * v[e];
-    }
+    for (int e = 0; e < 4; ++e) o[e] += w * v[e];
   }
   const float inv = 1.0f / l;
-  half* dst = out + (size_t)(mg.z + q) * HIDDEN + h * HDIM + d0;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const half4 w4 = {(half)(o[4 * i] * inv), (half)(o[4 * i + 1] * inv), (half)(o[4 * i + 2] * inv),
-                      (half)(o[4 * i + 3] * inv)};
-    *reinterpret_cast<half4*>(dst + 4 * i) = w4;
-  }
+  const half4 w4 = {(half)(o[0] * inv), (half)(o[1] * inv), (half)(o[2] * inv), (half)(o[3] * inv)};
+  *reinterpret_cast<half4*>(out + (size_t)(mg.z + q) * HIDDEN + h * HDIM + d) = w4;
 }
 
 }  // namespace
@@ -384,6 +430,8 @@ int attention_splits(int t) {
 void rel_attention(const AttnArgs& a, hipStream_t stream) {
   BARK_REQUIRE(a.ntiles > 0 && a.tiles, "rel_attention: no query tiles");
   BARK_REQUIRE(a.mp % 64 == 0 && a.pp >= 2 * a.tc - 1, "rel_attention: bad buffer shape");
+  BARK_REQUIRE((long long)a.mp * HDIM < (1ll << 31) && (long long)a.pp * HDIM < (1ll << 31),
+               "rel_attention: per-head blocks must stay below 2^31 elements");
   static_assert(sizeof(Smem) <= 160 * 1024, "LDS budget");
   static_assert(K_CH * NT * 8 == BKV * HDIM && V_CH * NT * 8 == HDIM * BKV && R_NEW * NT * 8 == 64 * HDIM &&
                     R_CH * NT * 8 == BAND * HDIM,
@@ -401,7 +449,7 @@ void rel_attention(const AttnArgs& a, hipStream_t stream) {
 void rel_attention_merge(const AttnArgs& a, hipStream_t stream) {
   if (a.nmerges == 0) return;
   BARK_REQUIRE(a.merges && a.part_o && a.part_ml, "rel_attention_merge: missing partial buffers");
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.nmerges * HEADS), dim3(256), 0, stream, a.part_o, a.part_ml,
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.nmerges * HEADS * (BQ / MERGE_Q)), dim3(256), 0, stream, a.part_o, a.part_ml,
                      a.merges, a.out);
   BARK_HIP_CHECK(hipGetLastError());
 }
