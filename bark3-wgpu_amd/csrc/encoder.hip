@@ -205,7 +205,7 @@ struct BarkHip {
   // workspace
   DevBuf sub16, xn, hid, qu, qv, kh, vt, rk, ao, h, h2, glu, pooler, dump, bounds, tiles;
   DevBuf part;  // split-K partial sums of the residual linears
-  DevBuf merges, attn_po, attn_pml;  // attention key-range partials
+  DevBuf merges, attn_lanes, attn_po, attn_pml;  // attention work lanes and key-range partials
   DevBuf y1, y2, y3, y4, mel, subf32;
 
   template <class T>
@@ -219,7 +219,7 @@ struct BarkHip {
 
   void ensure(DevBuf& b, size_t bytes) {
     if (bytes <= b.cap) return;
-    if (&b == &bounds || &b == &tiles || &b == &merges) table_key.clear();
+    if (&b == &bounds || &b == &tiles || &b == &merges || &b == &attn_lanes) table_key.clear();
     BARK_HIP_CHECK(hipDeviceSynchronize());  // any stream may still use the old buffer
     if (b.p) BARK_HIP_CHECK(hipFree(b.p));
     b.p = nullptr;
@@ -238,7 +238,7 @@ struct BarkHip {
     for (void* p : allocs) (void)hipFree(p);
     DevBuf* bufs[] = {&pos, &sub16, &xn, &hid, &qu, &qv, &kh, &vt, &rk, &ao, &h, &h2, &glu, &part,
                       &pooler, &dump, &bounds, &tiles, &y1, &y2, &y3, &y4, &mel, &subf32,
-                      &merges, &attn_po, &attn_pml};
+                      &merges, &attn_lanes, &attn_po, &attn_pml};
     for (DevBuf* b : bufs)
       if (b->p) (void)hipFree(b->p);
     if (stream) (void)hipStreamDestroy(stream);
@@ -506,8 +506,10 @@ struct BarkHip {
     ensure(pooler, mp * PROJ * 4);
     ensure(bounds, mp * sizeof(int2));
     std::vector<int4> tl, ml;
-    attention_tables(pl, tl, ml);
+    std::vector<int> ll;
+    attention_tables(pl, tl, ll, ml);
     ensure(tiles, tl.size() * sizeof(int4));
+    ensure(attn_lanes, ll.size() * sizeof(int));
     ensure(merges, std::max<size_t>(ml.size(), 1) * sizeof(int4));
     if (!ml.empty()) {
       ensure(attn_po, tl.size() * HEADS * 128 * HDIM * 4);
@@ -516,19 +518,36 @@ struct BarkHip {
     ensure_pos(pl.tc);
   }
 
-  // Attention work list: per sequence, query tiles x key-range splits, and a
-  // merge entry for every query tile with more than one split.
-  static void attention_tables(const Plan& pl, std::vector<int4>& tl, std::vector<int4>& ml) {
+  // Attention work list. Per sequence, its query tile x key tile units (in
+  // query tile, then key tile order) are cut evenly over attention_lanes(t)
+  // workgroup lanes; a lane's range becomes one segment per query tile it
+  // touches, so the pieces of one query tile are consecutive segments, and a
+  // merge entry joins them when there is more than one.
+  static void attention_tables(const Plan& pl, std::vector<int4>& tl, std::vector<int>& ll,
+                               std::vector<int4>& ml) {
     for (const auto& s : pl.seqs) {
-      const int ntk = (s.t + 63) / 64;
-      const int tps = (ntk + attention_splits(s.t) - 1) / attention_splits(s.t);  // key tiles per split
-      const int ns = (ntk + tps - 1) / tps;
-      for (int q0 = 0; q0 < s.t; q0 += 128) {
-        if (ns > 1) ml.push_back(make_int4((int)tl.size(), ns, s.start + q0, std::min(128, s.t - q0)));
-        for (int i = 0; i < ns; ++i)
-          tl.push_back(make_int4(s.start, s.t, q0, (i * tps) | (std::min(ntk, (i + 1) * tps) << 16)));
+      const int ntk = (s.t + 63) / 64, nqt = (s.t + 127) / 128;
+      const long units = (long)nqt * ntk;
+      const int lanes = attention_lanes(s.t);
+      const size_t first = tl.size();
+      for (int l = 0; l < lanes; ++l) {
+        ll.push_back((int)tl.size());
+        const long u1 = units * (l + 1) / lanes;
+        for (long u = units * l / lanes; u < u1;) {
+          const int qi = (int)(u / ntk), kb = (int)(u % ntk);
+          const int ke = (int)std::min<long>(ntk, kb + (u1 - u));
+          tl.push_back(make_int4(s.start, s.t, qi * 128, kb | (ke << 16)));
+          u += ke - kb;
+        }
+      }
+      for (size_t i = first; i < tl.size();) {
+        size_t j = i + 1;
+        while (j < tl.size() && tl[j].z == tl[i].z) ++j;
+        if (j - i > 1) ml.push_back(make_int4((int)i, (int)(j - i), s.start + tl[i].z, std::min(128, s.t - tl[i].z)));
+        i = j;
       }
     }
+    ll.push_back((int)tl.size());
   }
 
   // Row bounds for the depthwise conv and query tiles for attention.
@@ -544,7 +563,8 @@ struct BarkHip {
     for (const auto& s : pl.seqs)
       for (int r = s.start; r < s.start + s.t; ++r) b[r] = make_int2(s.start, s.start + s.t);
     std::vector<int4> tl, ml;
-    attention_tables(pl, tl, ml);
+    std::vector<int> ll;
+    attention_tables(pl, tl, ll, ml);
     BARK_HIP_CHECK(hipMemcpyAsync(bounds.p, b.data(), b.size() * sizeof(int2),
                                   hipMemcpyHostToDevice, st));
     BARK_HIP_CHECK(hipMemcpyAsync(tiles.p, tl.data(), tl.size() * sizeof(int4),
@@ -552,12 +572,16 @@ struct BarkHip {
     if (!ml.empty())
       BARK_HIP_CHECK(hipMemcpyAsync(merges.p, ml.data(), ml.size() * sizeof(int4),
                                     hipMemcpyHostToDevice, st));
+    BARK_HIP_CHECK(hipMemcpyAsync(attn_lanes.p, ll.data(), ll.size() * sizeof(int), hipMemcpyHostToDevice, st));
     ntiles = (int)tl.size();
+    nlanes = (int)ll.size() - 1;
     nmerges = (int)ml.size();
+    nparts = 0;
+    for (const auto& m : ml) nparts += m.y;
     BARK_HIP_CHECK(hipStreamSynchronize(st));  // host vectors go out of scope
     table_key = key;
   }
-  int ntiles = 0, nmerges = 0;
+  int ntiles = 0, nlanes = 0, nmerges = 0, nparts = 0;
 
   // Algorithmic bytes of a linear's weight operand.
   static double weight_bytes(const GemmWeight& w) {
@@ -688,12 +712,12 @@ struct BarkHip {
       gemm_op("qkv_heads", xnp, HIDDEN, mp, mr, L.qkv, Epi::Qkv, e, 2.0 * 4096, st);
       AttnArgs aa{qu.as<half>(), qv.as<half>(), kh.as<half>(), vt.as<half>(),
                   rk.as<half>() + (size_t)l * HEADS * pp * HDIM,
-                  ao.as<half>(), mp, pp, tc, tiles.as<int4>(), ntiles,
+                  ao.as<half>(), mp, pp, tc, tiles.as<int4>(), ntiles, attn_lanes.as<int>(), nlanes,
                   attn_po.as<float>(), attn_pml.as<float>(), merges.as<int4>(), nmerges};
       prof.run("rel_attention", attn_flops, 2.0 * mr * HIDDEN * 5 + 2.0 * prows * HIDDEN, st,
                [&] { rel_attention(aa, st); });
       if (nmerges)  // partial (o, max, sum) of every split query tile -> heads-flat f16
-        prof.run("attn_merge", 0, (double)ntiles * HEADS * 128 * (HDIM + 2) * 4 + 2.0 * mr * HIDDEN, st,
+        prof.run("attn_merge", 0, (double)nparts * HEADS * 128 * (HDIM + 2) * 4 + 2.0 * mr * HIDDEN, st,
                  [&] { rel_attention_merge(aa, st); });
       res = resid_op("attn_out_resid", ao.as<half>(), HIDDEN, mp, mr, L.o, 1.0f, st);
       // ---- conv module

@@ -83,27 +83,33 @@ struct ResidIn {
 };
 
 // ----------------------------------------------------------- attention --
-// One entry per (128-query tile, key range): {row of the sequence's first
-// frame, sequence length, first query of the tile (local), first key tile |
-// (end key tile << 16)} with 64-key tiles. An entry covering all keys writes
-// the output; otherwise it writes its unnormalised partial (o, max, sum) to
-// slot = entry index, and one merge entry {first slot, number of slots, first
-// output row, valid rows} combines the slots of a query tile in slot order.
+// Work is cut into segments {row of the sequence's first frame, sequence
+// length, first query of the 128-query tile (local), first key tile | (end key
+// tile << 16)} with 64-key tiles. Workgroup lane l (one per head) runs segments
+// lanes[l] .. lanes[l + 1] - 1 in order. A segment covering all keys of its
+// query tile writes the output; otherwise it writes its unnormalised partial
+// (o, max, sum) to slot = segment index, and one merge entry {first slot,
+// number of slots, first output row, valid rows} combines the consecutive
+// slots of a query tile in slot order.
 struct AttnArgs {
   const half *qu, *qv, *kh, *vt, *rk;
   half* out;       // (mp, 1024) heads-flat
   int mp;          // rows of qu/qv/kh and columns of vt
   int pp;          // rows of rk per head
   int tc;          // rk row j <-> relative position r = tc - 1 - j
-  const int4* tiles;
+  const int4* tiles;  // segments
   int ntiles;
+  const int* lanes;   // nlanes + 1 segment offsets
+  int nlanes;
   float* part_o = nullptr;   // [slot][head][128 q][128 d]
   float* part_ml = nullptr;  // [slot][head][128 q][2] (max, sum)
   const int4* merges = nullptr;
   int nmerges = 0;
 };
-// Key-range splits of one sequence's attention (a function of its length only).
-int attention_splits(int t);
+// Workgroup lanes per head for one sequence of length t (a function of t
+// only, so a sequence's arithmetic does not depend on the rest of its batch):
+// its query tile x key tile units are spread evenly over the lanes.
+int attention_lanes(int t);
 // q+u and q+v must be pre-multiplied by attention_q_scale() = log2(e)/sqrt(128)
 // (the Qkv epilogue does it when EpiArgs::scale is set to this value).
 // rel_attention writes the complete query tiles and the partials of split
