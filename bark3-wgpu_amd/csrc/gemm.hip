@@ -413,9 +413,20 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int l32 = lane & 31, lhi = lane >> 5;
-  const int n0 = blockIdx.x * 256, m0 = blockIdx.y * BM;
+  // XCD-aware tile order: the hardware hands block b to XCD b % 8, so block
+  // ids are renumbered to give each XCD a contiguous run of tiles in (split,
+  // row tile, column tile) order. All column tiles of a row tile then share
+  // one XCD's L2 for their A rows (read once per row tile instead of once per
+  // column tile). Which tile a workgroup computes does not change its results.
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int G = gx * gy * gridDim.z;
+  const int bid = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const int xq = G / 8, xr = G % 8, xcd = bid % 8;
+  const int tix = xcd * xq + min(xcd, xr) + bid / 8;
+  const int bz = tix / (gx * gy), by = (tix / gx) % gy, bx = tix % gx;
+  const int n0 = bx * 256, m0 = by * BM;
   const int nw = n0 + wid * 64;
-  const int kz0 = blockIdx.z * p.kc;  // first k of this split
+  const int kz0 = bz * p.kc;  // first k of this split
 
   // Global addresses are a wave-uniform base plus 32-bit lane offsets (the
   // host checks the operands fit), so loads use scalar base registers.
@@ -585,7 +596,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   // per column; row offsets are compile-time multiples of the row stride; a
   // tile inside M skips the per-row bound checks.
   EpiArgs ea = p.ea;
-  if constexpr (EPI == (int)Epi::StoreF32) ea.out_f32 += blockIdx.z * p.out_zstride;
+  if constexpr (EPI == (int)Epi::StoreF32) ea.out_f32 += bz * p.out_zstride;
   const int mrow = m0 + 4 * lhi;  // row of acc element v = 0 of block i = 0
   auto epilogue = [&](auto checked) {
   constexpr bool CHK = decltype(checked)::value;
