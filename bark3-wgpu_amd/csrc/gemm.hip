@@ -462,11 +462,13 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
 
   // Loads past the last k-tile re-read it (no branch, stays in bounds).
   const int nk = p.kc / BK;
-  auto load_a = [&](int kt, AStage& a) {
+  auto load_a_chunk = [&](int kt, AStage& a, int i) {
     kt = min(kt, nk - 1);
-    const half* at = abase + kt * BK;
+    a.v[i] = *reinterpret_cast<const uint4*>(abase + kt * BK + aoff[i]);
+  };
+  auto load_a = [&](int kt, AStage& a) {
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) a.v[i] = *reinterpret_cast<const uint4*>(at + aoff[i]);
+    for (int i = 0; i < A_CH; ++i) load_a_chunk(kt, a, i);
   };
   auto load_b = [&](int kt, BStage& b) {
     kt = min(kt, nk - 1);
@@ -518,8 +520,12 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   };
 
   // One k-tile from LDS buffer `cur` and B stage `bs`; meanwhile stores the
-  // next tile's A (register stage `as`) into buffer `nxt`.
-  auto tile = [&](int cur, int nxt, const BStage& bs, const AStage& as) {
+  // next tile's A (register stage `as`) into buffer `nxt`, and issues the
+  // global loads of A k-tile `ka` into stage `ad` (slices 0-1) and of B k-tile
+  // `kb` into stage `bd` (slice 3, after the last code word of `bs` was
+  // expanded), spread between the MFMAs so the wave never stalls on a full
+  // load queue with the matrix core idle.
+  auto tile = [&](int cur, int nxt, const BStage& bs, const AStage& as, int ka, AStage& ad, int kb, BStage& bd) {
     half8 af[2][FM];
     half8 bf[2][2];
     constexpr int VEXP = LUT4 ? 50 : 1;  // VALU instructions of two code expansions
@@ -542,6 +548,17 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < A_CH; ++i)
         if (i * 4 / A_CH == s) store_chunk(nxt, as, i);
+      constexpr int A_LO = (A_CH + 1) / 2;
+      if (s == 0) {
+#pragma unroll
+        for (int i = 0; i < A_LO; ++i) load_a_chunk(ka, ad, i);
+      } else if (s == 1) {
+#pragma unroll
+        for (int i = A_LO; i < A_CH; ++i) load_a_chunk(ka, ad, i);
+      } else if (s == 3) {
+        load_b(kb, bd);
+      }
+      const int nvm = s == 0 ? A_LO : s == 1 ? A_CH - A_LO : s == 3 ? B_V : 0;  // loads this slice
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -551,14 +568,15 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
       for (int m = 0; m < 2 * FM; ++m) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         if (s < 3) __builtin_amdgcn_sched_group_barrier(0x002, VPER, 0);
+        if (m < nvm) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
   // Per k-tile kt: LDS buffer kt%2 holds A(kt); A(kt+1) is stored from its
-  // register stage during the tile; loads for A(kt+4) and B(kt+BD) refill the
-  // stages the tile freed. Past the end the stores repeat the last tile into
+  // register stage during the tile; loads for A(kt+AD) and B(kt+BD), issued
+  // during the tile, refill the stages it frees. Past the end the stores repeat the last tile into
   // a buffer that is never read again.
   load_a(0, ra0);
   load_b(0, rb0);
@@ -572,21 +590,14 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   for (int i = 0; i < A_CH; ++i) store_chunk(0, ra0, i);
   __syncthreads();
   for (int kt = 0; kt < nk; kt += 4) {
-    tile(0, 1, rb0, ra1);
-    load_a(kt + AD, ra0);
-    load_b(kt + BD, rb0);
+    tile(0, 1, rb0, ra1, kt + AD, ra0, kt + BD, rb0);
     __syncthreads();
-    tile(1, 0, rb1, AD == 4 ? ra2 : ra0);
-    load_a(kt + 1 + AD, ra1);
-    load_b(kt + 1 + BD, rb1);
+    tile(1, 0, rb1, AD == 4 ? ra2 : ra0, kt + 1 + AD, ra1, kt + 1 + BD, rb1);
     __syncthreads();
-    tile(0, 1, LUT4 ? rb2 : rb0, AD == 4 ? ra3 : ra1);
-    load_a(kt + 2 + AD, AD == 4 ? ra2 : ra0);
-    load_b(kt + 2 + BD, LUT4 ? rb2 : rb0);
+    tile(0, 1, LUT4 ? rb2 : rb0, AD == 4 ? ra3 : ra1, kt + 2 + AD, AD == 4 ? ra2 : ra0, kt + 2 + BD,
+         LUT4 ? rb2 : rb0);
     __syncthreads();
-    tile(1, 0, LUT4 ? rb3 : rb1, ra0);
-    load_a(kt + 3 + AD, AD == 4 ? ra3 : ra1);
-    load_b(kt + 3 + BD, LUT4 ? rb3 : rb1);
+    tile(1, 0, LUT4 ? rb3 : rb1, ra0, kt + 3 + AD, AD == 4 ? ra3 : ra1, kt + 3 + BD, LUT4 ? rb3 : rb1);
     __syncthreads();
   }
 
