@@ -403,12 +403,16 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
 // results for the same weight values. Per k-tile a wave runs 8*FM MFMAs
 // against 4*FM fragment reads (and 8 code expansions in 4-bit mode).
 template <int FM, bool LUT4, bool SWZ, bool ABF16, int EPI>
-__global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
+__global__ void __launch_bounds__(256, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kernel(GemmParams p) {
   constexpr int BM = 32 * FM;
   constexpr int A_CH = BM * BK / 8 / 256;  // 16-byte chunks of A per thread per k-tile (= FM)
   constexpr int B_V = LUT4 ? 2 : 8;        // 16-byte loads of B per lane per k-tile
-  constexpr int BD = LUT4 ? 4 : 2;         // k-tiles of B in flight (register stages)
-  constexpr int AD = FM >= 6 ? 2 : 4;      // k-tiles of A in flight (register stages)
+  // 4-bit tiles of up to 128 rows keep two workgroups per CU (two waves per
+  // SIMD, so one wave's code expansion overlaps the other's MFMAs): that needs
+  // <= 256 registers per lane, hence two register stages of A and B.
+  constexpr bool OCC2 = LUT4 && FM <= 4;
+  constexpr int BD = (LUT4 && !OCC2) ? 4 : 2;  // k-tiles of B in flight (register stages)
+  constexpr int AD = (FM >= 6 || OCC2) ? 2 : 4;  // k-tiles of A in flight (register stages)
   __shared__ __attribute__((aligned(16))) half As[2][BM * LDK];
 
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -458,7 +462,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
     uint4 v[B_V];
   };
   AStage ra0, ra1, ra2, ra3;
-  BStage rb0, rb1, rb2, rb3;  // f16 mode uses rb0/rb1 only
+  BStage rb0, rb1, rb2, rb3;  // rb2/rb3 only with four B stages
 
   // Loads past the last k-tile re-read it (no branch, stays in bounds).
   const int nk = p.kc / BK;
@@ -583,9 +587,9 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
   load_a(1, ra1);
   load_b(1, rb1);
   if constexpr (AD == 4) load_a(2, ra2);
-  if constexpr (LUT4) load_b(2, rb2);
+  if constexpr (BD == 4) load_b(2, rb2);
   if constexpr (AD == 4) load_a(3, ra3);
-  if constexpr (LUT4) load_b(3, rb3);
+  if constexpr (BD == 4) load_b(3, rb3);
 #pragma unroll
   for (int i = 0; i < A_CH; ++i) store_chunk(0, ra0, i);
   __syncthreads();
@@ -594,10 +598,10 @@ __global__ void __launch_bounds__(256, 1) gemm_wide_kernel(GemmParams p) {
     __syncthreads();
     tile(1, 0, rb1, AD == 4 ? ra2 : ra0, kt + 1 + AD, ra1, kt + 1 + BD, rb1);
     __syncthreads();
-    tile(0, 1, LUT4 ? rb2 : rb0, AD == 4 ? ra3 : ra1, kt + 2 + AD, AD == 4 ? ra2 : ra0, kt + 2 + BD,
-         LUT4 ? rb2 : rb0);
+    tile(0, 1, BD == 4 ? rb2 : rb0, AD == 4 ? ra3 : ra1, kt + 2 + AD, AD == 4 ? ra2 : ra0, kt + 2 + BD,
+         BD == 4 ? rb2 : rb0);
     __syncthreads();
-    tile(1, 0, LUT4 ? rb3 : rb1, ra0, kt + 3 + AD, AD == 4 ? ra3 : ra1, kt + 3 + BD, LUT4 ? rb3 : rb1);
+    tile(1, 0, BD == 4 ? rb3 : rb1, ra0, kt + 3 + AD, AD == 4 ? ra3 : ra1, kt + 3 + BD, BD == 4 ? rb3 : rb1);
     __syncthreads();
   }
 
