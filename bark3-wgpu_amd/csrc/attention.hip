@@ -442,14 +442,14 @@ void rel_attention(const AttnArgs& a, hipStream_t stream) {
   }();
   BARK_REQUIRE(attr, "rel_attention: cannot reserve LDS");
   BARK_REQUIRE(a.nmerges == 0 || (a.merges && a.part_o && a.part_ml), "rel_attention: missing partial buffers");
-  hipLaunchKernelGGL(rel_attn_kernel, dim3(a.nlanes * HEADS), dim3(NT), sizeof(Smem), stream, a);
+  BARK_LAUNCH(rel_attn_kernel, dim3(a.nlanes * HEADS), dim3(NT), sizeof(Smem), stream, a);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
 void rel_attention_merge(const AttnArgs& a, hipStream_t stream) {
   if (a.nmerges == 0) return;
   BARK_REQUIRE(a.merges && a.part_o && a.part_ml, "rel_attention_merge: missing partial buffers");
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(a.nmerges * HEADS * (BQ / MERGE_Q)), dim3(256), 0, stream, a.part_o, a.part_ml,
+  BARK_LAUNCH(attn_merge_kernel, dim3(a.nmerges * HEADS * (BQ / MERGE_Q)), dim3(256), 0, stream, a.part_o, a.part_ml,
                      a.merges, a.out);
   BARK_HIP_CHECK(hipGetLastError());
 }

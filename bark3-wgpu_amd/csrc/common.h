@@ -1,6 +1,7 @@
 // Shared definitions for the gfx950 Conformer-encoder kernels.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -37,6 +38,28 @@ struct Error {
 #define BARK_REQUIRE(cond, text)                                                      \
   do {                                                                                \
     if (!(cond)) throw ::bark::Error{std::string(text)};                              \
+  } while (0)
+
+// Kernel timing for the per-op profiler. While `stop` is set, every launch
+// goes through hipExtLaunchKernelGGL with the events attached to the dispatch
+// itself (start on the op's first kernel, stop on each, so the last one wins):
+// the events then hold the kernels' own begin and end times, without the
+// dispatch gaps that separate marker events would add.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+  int launches = 0;
+};
+extern thread_local LaunchTiming g_launch_timing;
+
+#define BARK_LAUNCH(kernel, grid, block, shmem, stream, ...)                                  \
+  do {                                                                                        \
+    ::bark::LaunchTiming& lt_ = ::bark::g_launch_timing;                                      \
+    if (lt_.stop) {                                                                           \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, lt_.launches++ ? nullptr : lt_.start, \
+                            lt_.stop, 0, __VA_ARGS__);                                        \
+    } else {                                                                                  \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                    \
+    }                                                                                         \
   } while (0)
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }

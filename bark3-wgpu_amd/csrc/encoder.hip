@@ -21,6 +21,8 @@
 #include "kernels.h"
 
 namespace bark {
+thread_local LaunchTiming g_launch_timing;
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -120,10 +122,21 @@ struct Profiler {
       f();
       return;
     }
+    // the op's kernels carry the events themselves (BARK_LAUNCH)
     Op op{label, flops, bytes, take(), take()};
-    BARK_HIP_CHECK(hipEventRecord(op.a, st));
-    f();
-    BARK_HIP_CHECK(hipEventRecord(op.b, st));
+    g_launch_timing = LaunchTiming{op.a, op.b, 0};
+    try {
+      f();
+    } catch (...) {
+      g_launch_timing = LaunchTiming();
+      throw;
+    }
+    const int launched = g_launch_timing.launches;
+    g_launch_timing = LaunchTiming();
+    if (launched == 0) {  // nothing ran: an empty interval
+      BARK_HIP_CHECK(hipEventRecord(op.a, st));
+      BARK_HIP_CHECK(hipEventRecord(op.b, st));
+    }
     ops.push_back(op);
   }
   std::string report() {

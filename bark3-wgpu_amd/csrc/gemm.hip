@@ -795,7 +795,7 @@ template <int FM>
 void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t s) {
   dim3 grid(p.N / 256, ceil_div(p.M, 32 * FM), p.K / p.kc), block(256);
 #define BARK_K(L4, SW, AB, E) \
-  hipLaunchKernelGGL((gemm_wide_kernel<FM, L4, SW, AB, (int)Epi::E>), grid, block, 0, s, p)
+  BARK_LAUNCH((gemm_wide_kernel<FM, L4, SW, AB, (int)Epi::E>), grid, block, 0, s, p)
 #define BARK_CASE(E)                                   \
   case Epi::E:                                         \
     if (fmt == 0) BARK_K(false, false, false, E);      \
@@ -840,7 +840,7 @@ void launch_full(const GemmParams& p, Epi epi, hipStream_t s) {
   switch (epi) {
 #define BARK_CASE(E)                                                                          \
   case Epi::E:                                                                                \
-    hipLaunchKernelGGL((gemm_kernel<BM, LUT4, SWZ, false, (int)Epi::E>), grid, block, 0, s, p); \
+    BARK_LAUNCH((gemm_kernel<BM, LUT4, SWZ, false, (int)Epi::E>), grid, block, 0, s, p); \
     break;
     BARK_CASE(StoreF32)
     BARK_CASE(StoreF16)
@@ -864,9 +864,9 @@ void launch_plain(const GemmParams& p, Epi epi, bool abf16, hipStream_t s) {
 #define BARK_CASE(E)                                                                              \
   case Epi::E:                                                                                    \
     if (abf16)                                                                                    \
-      hipLaunchKernelGGL((gemm_kernel<BM, true, false, true, (int)Epi::E>), grid, block, 0, s, p);  \
+      BARK_LAUNCH((gemm_kernel<BM, true, false, true, (int)Epi::E>), grid, block, 0, s, p);  \
     else                                                                                          \
-      hipLaunchKernelGGL((gemm_kernel<BM, true, false, false, (int)Epi::E>), grid, block, 0, s, p); \
+      BARK_LAUNCH((gemm_kernel<BM, true, false, false, (int)Epi::E>), grid, block, 0, s, p); \
     break;
   switch (epi) {
     BARK_CASE(StoreF32)
@@ -1047,7 +1047,7 @@ void gemm_isolated(const half* A, int M, const GemmWeight& W, void* C, int c_kin
   float* part = isolated_workspace(stream, splits * stride * sizeof(float));
   gemm_split(A, W.k, M, W, splits, part, W.n, stream, a_bf16);
   const long n4 = (long)(stride / 4);
-  hipLaunchKernelGGL(split_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream, part,
+  BARK_LAUNCH(split_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream, part,
                      splits, stride, C, c_kind, n4);
   BARK_HIP_CHECK(hipGetLastError());
 }

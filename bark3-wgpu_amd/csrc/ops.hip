@@ -307,7 +307,7 @@ void layer_norm(float* x, const float* w, const float* b, half* y16, float* y32,
                 hipStream_t stream, const ResidIn& res) {
   if (rows <= 0) return;
   check_resid(res);
-  hipLaunchKernelGGL(ln_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, w, b, y16,
+  BARK_LAUNCH(ln_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, w, b, y16,
                      y32, rows, res);
   BARK_HIP_CHECK(hipGetLastError());
 }
@@ -316,7 +316,7 @@ void layer_norm2(const float* x, const float* wa, const float* ba, float* y32, c
                  const float* bb, half* y16, int rows, hipStream_t stream, const ResidIn& res) {
   if (rows <= 0) return;
   check_resid(res);
-  hipLaunchKernelGGL(ln2_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, wa, ba,
+  BARK_LAUNCH(ln2_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, wa, ba,
                      y32, wb, bb, y16, rows, res);
   BARK_HIP_CHECK(hipGetLastError());
 }
@@ -324,28 +324,28 @@ void layer_norm2(const float* x, const float* wa, const float* ba, float* y32, c
 void apply_residual(float* x, int rows, const ResidIn& res, hipStream_t stream) {
   if (rows <= 0 || res.splits == 0) return;
   check_resid(res);
-  hipLaunchKernelGGL(resid_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, rows, res);
+  BARK_LAUNCH(resid_kernel, dim3(ceil_div(rows, 4)), dim3(256), 0, stream, x, rows, res);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
 void dwconv_bn_silu(const float* g, const float* dw, const float* bn_a, const float* bn_b,
                     const int2* bounds, half* out, int rows, hipStream_t stream) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(dwconv_kernel, dim3(ceil_div(rows, 4 * DW_ROWS), HIDDEN / 256), dim3(256), 0,
+  BARK_LAUNCH(dwconv_kernel, dim3(ceil_div(rows, 4 * DW_ROWS), HIDDEN / 256), dim3(256), 0,
                      stream, g, dw, bn_a, bn_b, bounds, out, rows);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
 void f32_to_f16(const float* x, half* y, size_t n, hipStream_t stream) {
   if (n == 0) return;
-  hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+  BARK_LAUNCH(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                      x, y, n);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
 void f32_to_f16_rows(const float* x, int rows, int cols, half* y, int ldy, hipStream_t stream) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(f32_to_f16_rows_kernel, dim3(ceil_div(cols, 256), rows), dim3(256), 0,
+  BARK_LAUNCH(f32_to_f16_rows_kernel, dim3(ceil_div(cols, 256), rows), dim3(256), 0,
                      stream, x, cols, y, ldy, rows);
   BARK_HIP_CHECK(hipGetLastError());
 }
@@ -353,7 +353,7 @@ void f32_to_f16_rows(const float* x, int rows, int cols, half* y, int ldy, hipSt
 void copy_rows_f32(const float* x, int ldx, float* y, int ldy, int rows, int cols,
                    hipStream_t stream) {
   if (rows <= 0) return;
-  hipLaunchKernelGGL(copy_rows_kernel, dim3(ceil_div(cols, 256), rows), dim3(256), 0, stream, x,
+  BARK_LAUNCH(copy_rows_kernel, dim3(ceil_div(cols, 256), rows), dim3(256), 0, stream, x,
                      ldx, y, ldy, cols);
   BARK_HIP_CHECK(hipGetLastError());
 }
@@ -361,7 +361,7 @@ void copy_rows_f32(const float* x, int ldx, float* y, int ldy, int rows, int col
 void sub_conv1(const float* mel, int frames, const float* w, const float* b, half* out,
                int vlen, hipStream_t stream) {
   const int f1 = (frames - 1) / 2 + 1;
-  hipLaunchKernelGGL(conv1_kernel, dim3(64 / C1_PIX, f1), dim3(256), 0, stream, mel, frames, w,
+  BARK_LAUNCH(conv1_kernel, dim3(64 / C1_PIX, f1), dim3(256), 0, stream, mel, frames, w,
                      b, out, vlen);
   BARK_HIP_CHECK(hipGetLastError());
 }
@@ -369,7 +369,7 @@ void sub_conv1(const float* mel, int frames, const float* w, const float* b, hal
 void sub_dwconv(const half* in, int t_in, int m_in, const float* w, const float* b, half* out,
                 int vlen, hipStream_t stream) {
   const int t_out = (t_in - 1) / 2 + 1, m_out = (m_in - 1) / 2 + 1;
-  hipLaunchKernelGGL(sub_dw_kernel, dim3(ceil_div(t_out * m_out, DW2_PIX)), dim3(256), 0,
+  BARK_LAUNCH(sub_dw_kernel, dim3(ceil_div(t_out * m_out, DW2_PIX)), dim3(256), 0,
                      stream, in, t_in, m_in, w, b, out, t_out, m_out, vlen);
   BARK_HIP_CHECK(hipGetLastError());
 }
