@@ -1023,12 +1023,16 @@ float* isolated_workspace(hipStream_t stream, size_t bytes) {
 void gemm_isolated(const half* A, int M, const GemmWeight& W, void* C, int c_kind, hipStream_t stream,
                    bool a_bf16) {
   BARK_REQUIRE(c_kind >= 0 && c_kind <= 2, "gemm_isolated: bad output kind");
-  // Split K when the output tiles alone leave most CUs idle (small T): the
-  // chunks' partial sums go to a workspace and one pass adds them in order.
+  // Split K when the output tiles alone leave most CUs idle: at small T as
+  // far as the CUs fill, and in two for a long K whose 128-row tiles cover
+  // fewer than half of them (T = 2207, K = 4096, N = 1024). The chunks'
+  // partial sums go to a workspace and one pass adds them in order.
   const long base = (long)ceil_div(M, 64) * (W.n / 256);
   int splits = 1;
   if (W.n % 256 == 0 && base < 128) {
     while (splits * 2 * base <= 256 && W.k % (splits * 2) == 0 && (W.k / (splits * 2)) % 256 == 0) splits *= 2;
+  } else if (W.n % 256 == 0 && W.k >= 2048 && W.k % 512 == 0 && (long)ceil_div(M, 128) * (W.n / 256) < 128) {
+    splits = 2;
   }
   if (splits == 1) {
     EpiArgs e;
