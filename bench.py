@@ -9,9 +9,10 @@ already resident in HBM. value = audio seconds per second (encoder RTFx).
 
 Also reported:
   roofline     - the dominant kernel of the step (found in a separate pass
-                 that times every launch), from HIP events recorded on the
-                 library's stream around its launches only, during the timed
-                 region;
+                 that times every launch), from HIP events attached to its
+                 dispatches on the library's stream during the timed region
+                 (every 8th launch of it, so the timing adds ~0.5 % to the
+                 step);
   breakdown    - per-operator times from that separate all-launch pass;
   gemm_lowbit  - the isolated 4-bit linear of configs[1] (bf16 activations,
                  bf16 out) at T in {188, 2207}, rotating >256 MB of distinct

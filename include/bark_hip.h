@@ -113,7 +113,9 @@ int bark_hip_encode_mel_batch_device(BarkHip *h, const float *d_mel, const int32
 int bark_hip_profile(BarkHip *h, int enable);
 /* Restricts the per-operator timing to launches labelled `label` (NULL or ""
  * = every launch), so a benchmark can time one kernel inside its timed region
- * without bracketing all the others. Discards what was recorded. */
+ * without timing all the others; with a label, every 8th launch of it is
+ * timed (a timed launch costs a few microseconds of dispatch). Discards what
+ * was recorded. */
 int bark_hip_profile_only(BarkHip *h, const char *label);
 /* Writes JSON {label: {count, ms, flops, bytes}} aggregated over everything
  * recorded since the last report (flops/bytes are the algorithmic work of the
