@@ -48,7 +48,8 @@ struct GemmParams {
   const half* lut;
   int M, N, K;
   EpiArgs ea;
-  int kc = 0;            // wide kernel: k per split (blockIdx.z selects the chunk)
+  int splits = 1;        // wide kernel: K chunks (blockIdx.z selects one); chunk s covers
+                         // 256-k units [s*q + min(s, r), ...) of K/256 = q*splits + r
   size_t out_zstride = 0;  // wide kernel: elements between the splits' outputs
 };
 
@@ -430,7 +431,11 @@ __global__ void __launch_bounds__(256, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kern
   const int bz = tix / (gx * gy), by = (tix / gx) % gy, bx = tix % gx;
   const int n0 = bx * 256, m0 = by * BM;
   const int nw = n0 + wid * 64;
-  const int kz0 = bz * p.kc;  // first k of this split
+  // K chunk of this split: whole 256-k units, the first K/256 % splits
+  // chunks one unit longer (depends on K and the split count only)
+  const int kunits = p.K / 256, kq = kunits / p.splits, kr = kunits % p.splits;
+  const int kz0 = 256 * (bz * kq + min(bz, kr));  // first k of this split
+  const int kc = 256 * (kq + (bz < kr ? 1 : 0));   // k of this split
 
   // Global addresses are a wave-uniform base plus 32-bit lane offsets (the
   // host checks the operands fit), so loads use scalar base registers.
@@ -465,7 +470,7 @@ __global__ void __launch_bounds__(256, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kern
   BStage rb0, rb1, rb2, rb3;  // rb2/rb3 only with four B stages
 
   // Loads past the last k-tile re-read it (no branch, stays in bounds).
-  const int nk = p.kc / BK;
+  const int nk = kc / BK;
   auto load_a_chunk = [&](int kt, AStage& a, int i) {
     kt = min(kt, nk - 1);
     a.v[i] = *reinterpret_cast<const uint4*>(abase + kt * BK + aoff[i]);
@@ -793,7 +798,7 @@ bool wide_supported(Epi epi, int fmt) {
 
 template <int FM>
 void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t s) {
-  dim3 grid(p.N / 256, ceil_div(p.M, 32 * FM), p.K / p.kc), block(256);
+  dim3 grid(p.N / 256, ceil_div(p.M, 32 * FM), p.splits), block(256);
 #define BARK_K(L4, SW, AB, E) \
   BARK_LAUNCH((gemm_wide_kernel<FM, L4, SW, AB, (int)Epi::E>), grid, block, 0, s, p)
 #define BARK_CASE(E)                                   \
@@ -932,7 +937,7 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   BARK_REQUIRE(M > 0, "gemm: M must be positive");
   BARK_REQUIRE(lda >= W.k && lda % 8 == 0, "gemm: lda must be >= K and a multiple of 8");
   BARK_REQUIRE(W.lut4() ? (W.lut != nullptr) : (W.w16 != nullptr), "gemm: weight not set");
-  GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, W.k, 0};
+  GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, 1, 0};
   BARK_REQUIRE(!a_bf16 || (W.lut4() && !W.swizzled), "gemm: bf16 activations need plain 4-bit weights");
   const bool fits32 = (double)M * lda * 2 < 4.0e9 && (double)W.n * W.k * 2 < 4.0e9;
   const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
@@ -956,8 +961,8 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
 void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, float* part,
                 int ldo, hipStream_t stream, bool a_bf16) {
   BARK_REQUIRE(A != nullptr && part != nullptr, "gemm_split: null operand");
-  BARK_REQUIRE(splits >= 1 && W.k % splits == 0 && (W.k / splits) % (4 * BK) == 0,
-               "gemm_split: K / splits must be a positive multiple of 256");
+  BARK_REQUIRE(splits >= 1 && W.k % (4 * BK) == 0 && W.k / (4 * BK) >= splits,
+               "gemm_split: K must be a multiple of 256 with at least 256 per split");
   BARK_REQUIRE(W.n % 256 == 0 && W.n > 0, "gemm_split: N must be a positive multiple of 256");
   BARK_REQUIRE(M > 0 && ldo >= W.n, "gemm_split: bad M or ldo");
   BARK_REQUIRE(lda >= W.k && lda % 8 == 0, "gemm_split: lda must be >= K and a multiple of 8");
@@ -968,7 +973,7 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
   EpiArgs ea;
   ea.out_f32 = part;
   ea.ldo = ldo;
-  GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, W.k / splits, (size_t)M * ldo};
+  GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, splits, (size_t)M * ldo};
   const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
   int fm = pick_wide_fm(M, W.n, W.k, splits);
   if (fm == 0) fm = 2;
@@ -993,8 +998,8 @@ int residual_splits(int n, int k) {
   }();
   int s = 1;
   if (n == 1024 && k == 1024) s = f1 ? f1 : 2;
-  if (n == 1024 && k == 4096) s = f4 ? f4 : 2;
-  while (s > 1 && (k % s != 0 || (k / s) % 256 != 0)) --s;
+  if (n == 1024 && k == 4096) s = f4 ? f4 : 3;  // 6 + 5 + 5 units: 216 tiles of 128 rows at T = 2207
+  while (s > 1 && (k % 256 != 0 || k / 256 < s)) --s;
   return s;
 }
 

@@ -59,8 +59,9 @@ void swizzle_codes(uint8_t* codes, size_t nbytes);
 void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const EpiArgs& ea,
           hipStream_t stream, bool a_bf16 = false);
 
-// Split-K GEMM into partial sums: K is cut into `splits` equal chunks (each a
-// multiple of 256) and chunk s writes its f32 product to
+// Split-K GEMM into partial sums: K is cut into `splits` chunks of whole
+// 256-k units (the first K/256 % splits chunks one unit longer) and chunk s
+// writes its f32 product to
 // part + s * M * ldo (row stride ldo). The consumer adds the chunks in order
 // s = 0, 1, ... (see ResidIn), so the result depends on (N, K, splits) only,
 // never on M or on which workgroup finished first.
