@@ -889,20 +889,20 @@ void launch_plain(const GemmParams& p, Epi epi, bool abf16, hipStream_t s) {
 // counting every round) x (its relative per-CU rate); the best score wins.
 // Two-block tiles run two workgroups per CU once there are more than one per
 // CU. Rates and the short-K rule are from sweeps of the encoder shapes on
-// MI355X. BARK_HIP_GEMM_WIDE = 0/2/4/6/8 forces a choice.
+// MI355X. BARK_HIP_GEMM_WIDE = 0/2/3/4/5/6/8 forces a choice.
 int pick_wide_fm(int M, int N, int K, int splits = 1) {
   static const int forced = [] {
     const char* e = getenv("BARK_HIP_GEMM_WIDE");
     return e ? atoi(e) : -1;
   }();
-  if (forced == 0 || forced == 2 || forced == 4 || forced == 6 || forced == 8) return forced;
+  if (forced == 0 || (forced >= 2 && forced <= 6) || forced == 8) return forced;
   constexpr int CUS = 256;
   if (K / splits <= 256) return 2;  // a few k-tiles: the prologue dominates
   int best = 2;
   double best_score = -1.0;
-  const int fms[4] = {2, 4, 6, 8};
-  const double rate[4] = {0.9, 1.0, 1.1, 1.15};
-  for (int i = 0; i < 4; ++i) {
+  const int fms[6] = {2, 3, 4, 5, 6, 8};
+  const double rate[6] = {0.9, 0.95, 1.0, 1.05, 1.1, 1.15};
+  for (int i = 0; i < 6; ++i) {
     const long tiles = (long)ceil_div(M, 32 * fms[i]) * (N / 256) * splits;
     const long slots = (fms[i] == 2 && tiles > CUS) ? 2 * CUS : CUS;
     const long rounds = (tiles + slots - 1) / slots;
@@ -945,7 +945,9 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   if (fm) {
     if (fm == 8) launch_wide<8>(p, epi, fmt, a_bf16, stream);
     else if (fm == 6) launch_wide<6>(p, epi, fmt, a_bf16, stream);
+    else if (fm == 5) launch_wide<5>(p, epi, fmt, a_bf16, stream);
     else if (fm == 4) launch_wide<4>(p, epi, fmt, a_bf16, stream);
+    else if (fm == 3) launch_wide<3>(p, epi, fmt, a_bf16, stream);
     else launch_wide<2>(p, epi, fmt, a_bf16, stream);
     BARK_HIP_CHECK(hipGetLastError());
     return;
@@ -979,7 +981,9 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
   if (fm == 0) fm = 2;
   if (fm == 8) launch_wide<8>(p, Epi::StoreF32, fmt, a_bf16, stream);
   else if (fm == 6) launch_wide<6>(p, Epi::StoreF32, fmt, a_bf16, stream);
+  else if (fm == 5) launch_wide<5>(p, Epi::StoreF32, fmt, a_bf16, stream);
   else if (fm == 4) launch_wide<4>(p, Epi::StoreF32, fmt, a_bf16, stream);
+  else if (fm == 3) launch_wide<3>(p, Epi::StoreF32, fmt, a_bf16, stream);
   else launch_wide<2>(p, Epi::StoreF32, fmt, a_bf16, stream);
   BARK_HIP_CHECK(hipGetLastError());
 }
