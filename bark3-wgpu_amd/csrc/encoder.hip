@@ -225,7 +225,7 @@ struct BarkHip {
   DevBuf sub16, xn, hid, qu, qv, kh, vt, rk, ao, h, h2, glu, pooler, dump, bounds, tiles;
   DevBuf part;  // split-K partial sums of the residual linears
   DevBuf merges, attn_lanes, attn_po, attn_pml;  // attention work lanes and key-range partials
-  DevBuf y1, y2, y3, y4, mel, subf32;
+  DevBuf y2, y3, y4, mel, subf32;
 
   template <class T>
   T* upload(const T* src, size_t n) {
@@ -256,7 +256,7 @@ struct BarkHip {
     if (stream) (void)hipStreamSynchronize(stream);
     for (void* p : allocs) (void)hipFree(p);
     DevBuf* bufs[] = {&pos, &sub16, &xn, &hid, &qu, &qv, &kh, &vt, &rk, &ao, &h, &h2, &glu, &part,
-                      &pooler, &dump, &bounds, &tiles, &y1, &y2, &y3, &y4, &mel, &subf32,
+                      &pooler, &dump, &bounds, &tiles, &y2, &y3, &y4, &mel, &subf32,
                       &merges, &attn_lanes, &attn_po, &attn_pml};
     for (DevBuf* b : bufs)
       if (b->p) (void)hipFree(b->p);
@@ -638,12 +638,10 @@ struct BarkHip {
     const int f1 = conv_len(s.frames), t2 = conv_len(f1), t3 = conv_len(t2);
     int vlen = conv_len(std::max(s.valid, 1));
     const double p1 = (double)f1 * 64, p2 = (double)t2 * 32, p3 = (double)t3 * 16;
-    prof.run("fe_conv1", 2.0 * 9 * 256 * p1, 4.0 * s.frames * MEL + 2.0 * 256 * p1, st, [&] {
-      sub_conv1(d_mel, s.frames, l0w, l0b, y1.as<half>(), std::min(vlen, f1), st);
-    });
+    const int vlen1 = std::min(vlen, f1);
     vlen = conv_len(vlen);
-    prof.run("fe_dwconv", 2.0 * 9 * 256 * p2, 2.0 * 256 * (p1 + p2), st, [&] {
-      sub_dwconv(y1.as<half>(), f1, 64, l2w, l2b, y2.as<half>(), std::min(vlen, t2), st);
+    prof.run("fe_conv1_dw", 2.0 * 9 * 256 * (p1 + p2), 4.0 * s.frames * MEL + 2.0 * 256 * p2, st, [&] {
+      sub_conv1_dw(d_mel, s.frames, l0w, l0b, vlen1, l2w, l2b, std::min(vlen, t2), y2.as<half>(), st);
     });
     EpiArgs e1;
     e1.out_f16 = y3.as<half>();
@@ -664,14 +662,12 @@ struct BarkHip {
   }
 
   void ensure_front_end(const Plan& pl) {
-    size_t n1 = 0, n2 = 0, n4 = 0;
+    size_t n2 = 0, n4 = 0;
     for (const auto& s : pl.seqs) {
       const int f1 = conv_len(s.frames), t2 = conv_len(f1), t3 = conv_len(t2);
-      n1 = std::max(n1, (size_t)f1 * 64 * SUB_CH);
       n2 = std::max(n2, (size_t)t2 * 32 * SUB_CH);
       n4 = std::max(n4, (size_t)t3 * 16 * SUB_CH);
     }
-    ensure(y1, n1 * 2);
     ensure(y2, n2 * 2);
     ensure(y3, n2 * 2);
     ensure(y4, n4 * 2);

@@ -140,9 +140,11 @@ void f32_to_f16_rows(const float* x, int rows, int cols, half* y, int ldy,
                      hipStream_t stream);
 void copy_rows_f32(const float* x, int ldx, float* y, int ldy, int rows, int cols,
                    hipStream_t stream);
-// Front end. conv1: mel (frames, 128) f32 -> (f1, 64, 256) f16, ReLU, rows >= vlen zeroed.
-void sub_conv1(const float* mel, int frames, const float* w, const float* b, half* out,
-               int vlen, hipStream_t stream);
+// Front end. conv1 (mel (frames, 128) f32 -> (f1, 64, 256), ReLU, rows >= vlen1
+// zeroed, f16) fused with the first depthwise 3x3 stride 2 -> (t2, 32, 256) f16,
+// rows >= vlen2 zeroed.
+void sub_conv1_dw(const float* mel, int frames, const float* w1, const float* b1, int vlen1,
+                  const float* wd, const float* bd, int vlen2, half* out, hipStream_t stream);
 // depthwise 3x3 stride 2 on (t_in, m_in, 256) -> (t_out, m_out, 256), rows >= vlen zeroed.
 void sub_dwconv(const half* in, int t_in, int m_in, const float* w, const float* b,
                 half* out, int vlen, hipStream_t stream);

@@ -213,40 +213,94 @@ __global__ void copy_rows_kernel(const float* x, int ldx, float* y, int ldy, int
 }
 
 // -------------------------------------------------------------- front end --
-// conv 1->256, 3x3, stride 2, pad 1, then ReLU (src/sub.rs:116-168). Output
-// layout is pixel-major with channels contiguous: out[(i*64 + j)*256 + c].
-// The sum is b + w0*x0 + ... + w8*x8 in tap order as fused multiply-adds (the
-// reference AXPY rounds each product first: an ulp per tap); rows i >= vlen
-// are zeroed (mask_time, src/sub.rs:288-300).
-constexpr int C1_PIX = 8;  // output pixels (along mel) per workgroup
+// conv 1->256, 3x3, stride 2, pad 1, then ReLU (src/sub.rs:116-168), fused
+// with the first depthwise 3x3 stride 2 (src/sub.rs:174-203): the conv1 map
+// (8828 x 64 x 256 f16 = 289 MB at 17656 frames) never goes to HBM. A
+// workgroup makes FD_ROWS output rows x 32 columns x FD_CH channels; it first
+// computes the 2 * FD_ROWS + 1 conv1 rows they read into LDS, as the f16 value
+// an unfused conv1 would store, then the depthwise sums from there. conv1 is
+// b + w0*x0 + ... + w8*x8 in tap order as fused multiply-adds (the reference
+// AXPY rounds each product first: an ulp per tap); conv1 rows >= vlen1 are
+// zeroed (mask_time, src/sub.rs:288-300); the depthwise sum runs over the
+// in-range taps in (ki, kj) order from its bias, and output rows >= vlen2 are
+// zeroed. Thread = 4 consecutive channels x a strided set of positions.
+constexpr int FD_ROWS = 4, FD_CH = 32;
+constexpr int FD_C1R = 2 * FD_ROWS + 1;  // conv1 rows per workgroup
+constexpr int FD_MELR = 2 * FD_C1R + 1;  // mel rows per workgroup
 
-__global__ void __launch_bounds__(256) conv1_kernel(const float* mel, int frames,
-                                                    const float* w, const float* b, half* out,
-                                                    int vlen) {
-  __shared__ float patch[3][2 * C1_PIX + 1];
-  const int i = blockIdx.y;               // output frame
-  const int j0 = blockIdx.x * C1_PIX;     // first output mel bin
-  const int c = threadIdx.x;
-  if (threadIdx.x < 3 * (2 * C1_PIX + 1)) {
-    const int pr = threadIdx.x / (2 * C1_PIX + 1), pc = threadIdx.x % (2 * C1_PIX + 1);
-    const int si = 2 * i + pr - 1, sj = 2 * j0 + pc - 1;
-    patch[pr][pc] = (si >= 0 && si < frames && sj >= 0 && sj < MEL) ? mel[(size_t)si * MEL + sj] : 0.0f;
+__global__ void __launch_bounds__(256) conv1_dw_kernel(const float* mel, int frames, int f1, int vlen1,
+                                                       const float* w1, const float* b1, const float* wd,
+                                                       const float* bd, half* out, int t2, int vlen2) {
+  __shared__ float patch[FD_MELR][MEL + 2];  // columns -1 .. 128, zero outside the mel
+  __shared__ __attribute__((aligned(16))) half c1[FD_C1R][64][FD_CH];
+  const int r0 = blockIdx.x * FD_ROWS;  // first output row
+  const int tid = threadIdx.x;
+  const int ii0 = 2 * r0 - 1;           // first conv1 row
+  const int mr0 = 2 * ii0 - 1;          // first mel row
+  for (int i = tid; i < FD_MELR * (MEL + 2); i += 256) {
+    const int r = i / (MEL + 2), ci = i % (MEL + 2);
+    const int si = mr0 + r, sj = ci - 1;
+    patch[r][ci] = (si >= 0 && si < frames && sj >= 0 && sj < MEL) ? mel[(size_t)si * MEL + sj] : 0.0f;
   }
   __syncthreads();
-  float wr[9];
+  const int cg = tid & 7, pg = tid >> 3;  // channel group (4 channels), position group
+  const int cl = 4 * cg, c = blockIdx.y * FD_CH + cl;
+  float w[4][9], bb[4];
+  {
 #pragma unroll
-  for (int t = 0; t < 9; ++t) wr[t] = w[c * 9 + t];
-  const float bias = b[c];
-  const bool masked = i >= vlen;
+    for (int e = 0; e < 4; ++e) {
 #pragma unroll
-  for (int p = 0; p < C1_PIX; ++p) {
-    float acc = bias;
+      for (int t = 0; t < 9; ++t) w[e][t] = w1[(c + e) * 9 + t];
+      bb[e] = b1[c + e];
+    }
+    for (int p = pg; p < FD_C1R * 64; p += 32) {
+      const int lr = p >> 6, j = p & 63;
+      const int ii = ii0 + lr;
+      if (ii < 0 || ii >= f1) continue;  // rows the depthwise conv never reads
+      float x[9];
 #pragma unroll
-    for (int t = 0; t < 9; ++t)
-      acc = fmaf(wr[t], patch[t / 3][2 * p + t % 3], acc);
-    acc = acc > 0.0f ? acc : 0.0f;
-    if (masked) acc = 0.0f;
-    out[((size_t)i * 64 + j0 + p) * SUB_CH + c] = (half)acc;
+      for (int t = 0; t < 9; ++t) x[t] = patch[2 * lr + t / 3][2 * j + t % 3];
+      half4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float acc = bb[e];
+#pragma unroll
+        for (int t = 0; t < 9; ++t) acc = fmaf(w[e][t], x[t], acc);
+        acc = acc > 0.0f ? acc : 0.0f;
+        if (ii >= vlen1) acc = 0.0f;
+        v[e] = (half)acc;
+      }
+      *reinterpret_cast<half4*>(&c1[lr][j][cl]) = v;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+#pragma unroll
+    for (int t = 0; t < 9; ++t) w[e][t] = wd[(c + e) * 9 + t];
+    bb[e] = bd[c + e];
+  }
+  for (int q = pg; q < FD_ROWS * 32; q += 32) {
+    const int i2 = r0 + (q >> 5), j2 = q & 31;  // row uniform per iteration
+    if (i2 >= t2) break;
+    float sacc[4] = {bb[0], bb[1], bb[2], bb[3]};
+#pragma unroll
+    for (int ki = 0; ki < 3; ++ki) {
+      const int ii = 2 * i2 + ki - 1;
+      if (ii < 0 || ii >= f1) continue;
+#pragma unroll
+      for (int kj = 0; kj < 3; ++kj) {
+        const int jj = 2 * j2 + kj - 1;
+        if (jj < 0 || jj >= 64) continue;
+        const half4 xv = *reinterpret_cast<const half4*>(&c1[ii - ii0][jj][cl]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sacc[e] = fmaf(w[e][ki * 3 + kj], (float)xv[e], sacc[e]);
+      }
+    }
+    half4 z;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) z[e] = (half)(i2 >= vlen2 ? 0.0f : sacc[e]);
+    *reinterpret_cast<half4*>(out + ((size_t)i2 * 32 + j2) * SUB_CH + c) = z;
   }
 }
 
@@ -358,11 +412,12 @@ void copy_rows_f32(const float* x, int ldx, float* y, int ldy, int rows, int col
   BARK_HIP_CHECK(hipGetLastError());
 }
 
-void sub_conv1(const float* mel, int frames, const float* w, const float* b, half* out,
-               int vlen, hipStream_t stream) {
-  const int f1 = (frames - 1) / 2 + 1;
-  BARK_LAUNCH(conv1_kernel, dim3(64 / C1_PIX, f1), dim3(256), 0, stream, mel, frames, w,
-                     b, out, vlen);
+void sub_conv1_dw(const float* mel, int frames, const float* w1, const float* b1, int vlen1,
+                  const float* wd, const float* bd, int vlen2, half* out, hipStream_t stream) {
+  const int f1 = (frames - 1) / 2 + 1, t2 = (f1 - 1) / 2 + 1;
+  static_assert(SUB_CH % FD_CH == 0, "channel chunks must tile the 256 channels");
+  BARK_LAUNCH(conv1_dw_kernel, dim3(ceil_div(t2, FD_ROWS), SUB_CH / FD_CH), dim3(256), 0, stream, mel, frames,
+              f1, vlen1, w1, b1, wd, bd, out, t2, vlen2);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
