@@ -139,6 +139,15 @@ _SIGS = {
             _c.c_void_p, _c.c_size_t, _c.c_void_p,
         ],
     ),
+    "bark_hip_set_mel_filters": (_c.c_int, [_c.c_void_p, _c.c_void_p]),
+    "bark_hip_mel": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_size_t, _c.c_void_p, _c.c_void_p],
+    ),
+    "bark_hip_mel_device": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_size_t, _c.c_void_p, _c.c_void_p, _c.c_void_p],
+    ),
     "bark_hip_profile": (_c.c_int, [_c.c_void_p, _c.c_int]),
     "bark_hip_profile_only": (_c.c_int, [_c.c_void_p, _c.c_char_p]),
     "bark_hip_profile_report": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_size_t]),
@@ -312,6 +321,44 @@ class HipEncoder:
             )
         )
         return t_out
+
+    def set_mel_filters(self, filters: Optional[np.ndarray] = None) -> None:
+        """MelFrontend::new (src/mel.rs:25): the 128 x 257 filterbank (default:
+        the slaney filterbank of mel.slaney_mel_filters)."""
+        if filters is None:
+            from .mel import slaney_mel_filters
+
+            filters = slaney_mel_filters()
+        f = np.ascontiguousarray(filters, dtype=np.float32)
+        if f.shape != (MEL, 257):
+            raise ValueError(f"mel filters must be ({MEL}, 257), got {f.shape}")
+        _check(lib().bark_hip_set_mel_filters(self._h, _ptr(f)))
+
+    def mel(self, wave: np.ndarray) -> tuple[np.ndarray, int, int]:
+        """MelFrontend::compute (src/mel.rs:41): (features (frames, 128) f32,
+        frames, valid) of a 16 kHz mono wave."""
+        w = np.ascontiguousarray(wave, dtype=np.float32)
+        if w.ndim != 1 or w.size == 0:
+            raise ValueError("wave must be a non-empty 1-D array")
+        nf = 1 + w.size // 160
+        out = np.empty((nf, MEL), np.float32)
+        fr = np.zeros(1, np.int32)
+        va = np.zeros(1, np.int32)
+        _check(lib().bark_hip_mel(self._h, _ptr(w), w.size, _ptr(out), out.size, _ptr(fr), _ptr(va)))
+        return out, int(fr[0]), int(va[0])
+
+    def mel_device(self, d_wave: int, n_samples: int, d_features: int, cap: int, stream: int = 0) -> tuple[int, int]:
+        """Device pointers in and out, queued on `stream` without synchronising;
+        returns (frames, valid)."""
+        fr = np.zeros(1, np.int32)
+        va = np.zeros(1, np.int32)
+        _check(
+            lib().bark_hip_mel_device(
+                self._h, ctypes.c_void_p(d_wave), int(n_samples), ctypes.c_void_p(d_features), int(cap), _ptr(fr),
+                _ptr(va), ctypes.c_void_p(stream) if stream else None,
+            )
+        )
+        return int(fr[0]), int(va[0])
 
     def profile(self, enable: bool = True) -> None:
         """Per-operator HIP-event timing of the forward (BARK3_ENC_PROFILE)."""

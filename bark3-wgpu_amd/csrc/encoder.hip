@@ -217,6 +217,65 @@ struct BarkHip {
   float *l5w = nullptr, *l5b = nullptr, *l6b = nullptr;
   std::vector<DevLayer> layers;
 
+  // log-mel front end: window, twiddles, sparse filterbank, scratch
+  DevBuf mel_window, mel_twid, mel_rows, mel_vals, mel_ws, mel_wave, mel_feat;
+  bool has_mel = false;
+
+  void set_mel_filters(const float* filters) {
+    constexpr int NB = 257;
+    std::vector<float> win(512, 0.0f);
+    for (int i = 0; i < 400; ++i) {  // symmetric Hann, as src/mel.rs:28-35 computes it in f32
+      const float a = 6.28318530717958647692f * (float)i / 399.0f;
+      win[56 + i] = 0.5f * (1.0f - std::cos(a));
+    }
+    std::vector<double> tw(512);
+    for (int k = 0; k < 256; ++k) {
+      tw[k] = std::cos(2.0 * M_PI * k / 512.0);
+      tw[256 + k] = std::sin(2.0 * M_PI * k / 512.0);
+    }
+    std::vector<int> rows(3 * MEL);
+    std::vector<float> vals;
+    for (int m = 0; m < MEL; ++m) {  // the nonzero range of each row (zeros inside add nothing)
+      int first = -1, last = -1;
+      for (int k = 0; k < NB; ++k)
+        if (filters[(size_t)m * NB + k] != 0.0f) {
+          if (first < 0) first = k;
+          last = k;
+        }
+      const int count = first < 0 ? 0 : last - first + 1;
+      rows[3 * m] = std::max(first, 0);
+      rows[3 * m + 1] = count;
+      rows[3 * m + 2] = (int)vals.size();
+      for (int k = 0; k < count; ++k) vals.push_back(filters[(size_t)m * NB + first + k]);
+    }
+    ensure(mel_window, win.size() * 4);
+    ensure(mel_twid, tw.size() * 8);
+    ensure(mel_rows, rows.size() * 4);
+    ensure(mel_vals, std::max<size_t>(vals.size(), 1) * 4);
+    BARK_HIP_CHECK(hipMemcpy(mel_window.p, win.data(), win.size() * 4, hipMemcpyHostToDevice));
+    BARK_HIP_CHECK(hipMemcpy(mel_twid.p, tw.data(), tw.size() * 8, hipMemcpyHostToDevice));
+    BARK_HIP_CHECK(hipMemcpy(mel_rows.p, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
+    if (!vals.empty()) BARK_HIP_CHECK(hipMemcpy(mel_vals.p, vals.data(), vals.size() * 4, hipMemcpyHostToDevice));
+    has_mel = true;
+  }
+
+  void run_mel(const float* d_wave, long n, float* d_out, size_t cap, int32_t* n_frames, int32_t* n_valid,
+               hipStream_t st) {
+    BARK_REQUIRE(has_mel, "bark_hip_set_mel_filters was not called");
+    BARK_REQUIRE(n > 0, "empty wave");
+    const int nf = mel_frames(n);
+    BARK_REQUIRE(cap >= (size_t)nf * MEL, "features buffer too small");
+    ensure(mel_ws, mel_workspace_bytes(n));
+    MelTables tb;
+    tb.window = mel_window.as<float>();
+    tb.twiddle = mel_twid.as<double>();
+    tb.rows = mel_rows.as<int>();
+    tb.vals = mel_vals.as<float>();
+    prof.run("mel", 0, 4.0 * n + 4.0 * nf * MEL * 3, st, [&] { mel_features(d_wave, n, tb, mel_ws.p, d_out, st); });
+    if (n_frames) *n_frames = nf;
+    if (n_valid) *n_valid = (int32_t)(n / 160);
+  }
+
   // position table rows for pos = pos_t-1 .. -(pos_t-1), f16, plus zero rows
   DevBuf pos;
   int pos_t = 0;
@@ -257,7 +316,8 @@ struct BarkHip {
     for (void* p : allocs) (void)hipFree(p);
     DevBuf* bufs[] = {&pos, &sub16, &xn, &hid, &qu, &qv, &kh, &vt, &rk, &ao, &h, &h2, &glu, &part,
                       &pooler, &dump, &bounds, &tiles, &y2, &y3, &y4, &mel, &subf32,
-                      &merges, &attn_lanes, &attn_po, &attn_pml};
+                      &merges, &attn_lanes, &attn_po, &attn_pml, &mel_window, &mel_twid,
+                      &mel_rows, &mel_vals, &mel_ws, &mel_wave, &mel_feat};
     for (DevBuf* b : bufs)
       if (b->p) (void)hipFree(b->p);
     if (stream) (void)hipStreamDestroy(stream);
@@ -1044,6 +1104,45 @@ int bark_hip_encode_mel_batch_device(BarkHip* h, const float* d_mel, const int32
     hipStream_t st = stream ? static_cast<hipStream_t>(stream) : h->stream;
     h->encode_mel_batch(d_mel, true, n_frames, n_valid, batch, t_out, d_pooler, true,
                         pooler_cap, st);
+  });
+}
+
+int bark_hip_set_mel_filters(BarkHip* h, const float* filters) {
+  return guarded([&] {
+    BARK_REQUIRE(h && filters, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    h->set_mel_filters(filters);
+  });
+}
+
+int bark_hip_mel(BarkHip* h, const float* wave, int64_t n_samples, float* features, size_t cap, int32_t* n_frames,
+                 int32_t* n_valid) {
+  return guarded([&] {
+    BARK_REQUIRE(h && wave && features, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    BARK_REQUIRE(n_samples > 0, "empty wave");
+    const size_t nf = (size_t)mel_frames(n_samples);
+    BARK_REQUIRE(cap >= nf * MEL, "features buffer too small");
+    h->ensure(h->mel_wave, (size_t)n_samples * 4);
+    h->ensure(h->mel_feat, nf * MEL * 4);
+    BARK_HIP_CHECK(hipMemcpyAsync(h->mel_wave.p, wave, (size_t)n_samples * 4, hipMemcpyHostToDevice, h->stream));
+    h->run_mel(h->mel_wave.as<float>(), (long)n_samples, h->mel_feat.as<float>(), nf * MEL, n_frames, n_valid,
+               h->stream);
+    BARK_HIP_CHECK(hipMemcpyAsync(features, h->mel_feat.p, nf * MEL * 4, hipMemcpyDeviceToHost, h->stream));
+    BARK_HIP_CHECK(hipStreamSynchronize(h->stream));
+  });
+}
+
+int bark_hip_mel_device(BarkHip* h, const float* d_wave, int64_t n_samples, float* d_features, size_t cap,
+                        int32_t* n_frames, int32_t* n_valid, void* stream) {
+  return guarded([&] {
+    BARK_REQUIRE(h && d_wave && d_features, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    hipStream_t st = stream ? static_cast<hipStream_t>(stream) : h->stream;
+    h->run_mel(d_wave, (long)n_samples, d_features, cap, n_frames, n_valid, st);
   });
 }
 

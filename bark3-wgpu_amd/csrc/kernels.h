@@ -149,4 +149,21 @@ void sub_conv1_dw(const float* mel, int frames, const float* w1, const float* b1
 void sub_dwconv(const half* in, int t_in, int m_in, const float* w, const float* b,
                 half* out, int vlen, hipStream_t stream);
 
+// ------------------------------------------------------------- log-mel --
+// Device tables of the log-mel front end (mel.hip): the 512-point window, the
+// FFT twiddles (f64: cos then sin of 2 pi k / 512, k < 256), per mel row {first
+// bin, bin count, offset into vals} of its nonzero filter range, and the
+// filter values of those ranges.
+struct MelTables {
+  const float* window = nullptr;
+  const double* twiddle = nullptr;
+  const int* rows = nullptr;
+  const float* vals = nullptr;
+};
+int mel_frames(long n_samples);               // 1 + n / 160
+size_t mel_workspace_bytes(long n_samples);   // scratch of mel_features
+// features (mel_frames(n) x 128 f32) of a 16 kHz wave, all on `st`
+void mel_features(const float* wave, long n_samples, const MelTables& tb, void* workspace, float* out,
+                  hipStream_t st);
+
 }  // namespace bark

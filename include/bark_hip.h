@@ -131,6 +131,24 @@ int bark_hip_lowbit_linear(const void *A, int32_t a_dtype, const uint8_t *codes,
                            const uint16_t *lut16, void *C, int32_t c_dtype, int32_t T,
                            int32_t K, int32_t N, void *stream);
 
+/* Log-mel front end, the counterpart of MelFrontend (src/mel.rs:10-140).
+ * bark_hip_set_mel_filters takes the 128 x 257 row-major f32 filterbank, as
+ * MelFrontend::new does (src/mel.rs:25; the reference loads it from
+ * data/mel_filters.f32, src/inference.rs:46,480). */
+int bark_hip_set_mel_filters(BarkHip *h, const float *filters);
+/* MelFrontend::compute (src/mel.rs:41): features of a 16 kHz mono wave of
+ * n_samples f32 samples. Writes n_frames = 1 + n/160 rows x 128 f32 into
+ * `features` (capacity `cap` floats; padded rows >= n_valid = n/160 are zero)
+ * and the two counts — the Features struct (src/mel.rs:17-22). Host buffers;
+ * synchronises. */
+int bark_hip_mel(BarkHip *h, const float *wave, int64_t n_samples, float *features, size_t cap,
+                 int32_t *n_frames, int32_t *n_valid);
+/* Device-resident form: d_wave and d_features are device pointers, work is
+ * queued on `stream` (hipStream_t; NULL = the handle's stream), no host copies,
+ * not synchronised; the output can feed bark_hip_encode_mel_batch_device. */
+int bark_hip_mel_device(BarkHip *h, const float *d_wave, int64_t n_samples, float *d_features, size_t cap,
+                        int32_t *n_frames, int32_t *n_valid, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
