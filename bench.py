@@ -132,6 +132,51 @@ def bench_gemm(pkg, torch, T: int, K: int, N: int, reps: int = 192):
             "mfma_frac": F / t / 1e12 / PEAK_F16_TFLOPS, "hbm_frac": B / t / 1e9 / PEAK_HBM_GBS}
 
 
+def mel_wave() -> "np.ndarray":
+    """Synthetic 16 kHz wave whose log-mel has the encoder workload's 17656 frames."""
+    n = 160 * (FRAMES - 1) + 100
+    rng = np.random.default_rng(0)
+    t = np.arange(n) / 16000.0
+    return (0.2 * np.sin(2 * np.pi * (300 + 40 * t) * t) + 0.02 * rng.standard_normal(n)).astype(np.float32)
+
+
+def bench_mel(pkg, torch, reps: int = 20):
+    """GPU log-mel front end (bark_hip_mel_device) on the workload's audio, wave
+    resident in HBM: per-call time from events attached to its kernels."""
+    wave = mel_wave()
+    enc = pkg.HipEncoder(0, 1)
+    enc.set_mel_filters()
+    d_w = torch.from_numpy(wave).cuda()
+    nf = 1 + wave.size // 160
+    d_out = torch.empty((nf, 128), dtype=torch.float32, device="cuda")
+    sp = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        enc.mel_device(d_w.data_ptr(), wave.size, d_out.data_ptr(), d_out.numel(), sp)
+    torch.cuda.synchronize()
+    enc.profile(True)
+    for _ in range(reps):
+        enc.mel_device(d_w.data_ptr(), wave.size, d_out.data_ptr(), d_out.numel(), sp)
+    torch.cuda.synchronize()
+    rep = enc.profile_report()["mel"]
+    enc.profile(False)
+    enc.close()
+    ms = rep["ms"] / rep["count"]
+    byts = rep["bytes"] / rep["count"]
+    return {"samples": int(wave.size), "frames": nf, "audio_s": wave.size / 16000.0, "gpu_ms": ms,
+            "audio_s_per_s": wave.size / 16000.0 / (ms / 1e3), "gbs": byts / (ms / 1e3) / 1e9}
+
+
+def cpu_mel(pkg) -> float:
+    """The numpy oracle's log-mel of the same wave (ms)."""
+    from oracle import mel as omel
+
+    filters = importlib.import_module("bark3_wgpu_amd.mel").slaney_mel_filters()
+    wave = mel_wave()
+    t0 = time.perf_counter()
+    omel.features(wave, filters)
+    return (time.perf_counter() - t0) * 1e3
+
+
 def cpu_baseline(synth, blocks: int):
     """Oracle timing on this host's cores. blocks == 24 runs the complete
     workload (front end over the 17656-frame mel, 24 blocks, projector);
@@ -256,8 +301,15 @@ def main() -> int:
                 log(f"[bench] lowbit linear T={t} K={k} N={n}: {r['us']:.2f} us, {r['tflops']:.1f} TFLOP/s, "
                     f"{r['gbs']:.0f} GB/s")
 
+    mel = bench_mel(pkg, torch)
+    log(f"[bench] log-mel front end: {mel['gpu_ms']:.3f} ms for {mel['audio_s']:.2f} s of audio "
+        f"({mel['audio_s_per_s']:.0f} audio s/s)")
+
     cpu = None
     if not args.no_cpu:
+        mel["cpu_ms"] = cpu_mel(pkg)
+        mel["cpu_kind"] = "port (numpy oracle, oracle/mel.py)"
+        log(f"[bench] log-mel on the CPU oracle: {mel['cpu_ms']:.1f} ms")
         t0 = time.time()
         cpu = cpu_baseline(synth, args.cpu_blocks)
         log(f"[bench] cpu baseline {cpu['value']:.2f} audio s/s ({time.time() - t0:.1f}s)")
@@ -283,6 +335,7 @@ def main() -> int:
                      "avg_launch_us": avg_s * 1e6},
         "breakdown": breakdown,
         "gemm_lowbit": gemm,
+        "mel_frontend": mel,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
