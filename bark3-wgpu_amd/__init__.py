@@ -148,6 +148,10 @@ _SIGS = {
         _c.c_int,
         [_c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_size_t, _c.c_void_p, _c.c_void_p, _c.c_void_p],
     ),
+    "bark_hip_encode_wave_batch": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_void_p, _c.c_size_t],
+    ),
     "bark_hip_profile": (_c.c_int, [_c.c_void_p, _c.c_int]),
     "bark_hip_profile_only": (_c.c_int, [_c.c_void_p, _c.c_char_p]),
     "bark_hip_profile_report": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_size_t]),
@@ -359,6 +363,23 @@ class HipEncoder:
             )
         )
         return int(fr[0]), int(va[0])
+
+    def encode_wave_batch(self, waves: Sequence[np.ndarray]) -> list[np.ndarray]:
+        """Log-mel of each 16 kHz wave and one batched encode (chunked
+        transcription's per-chunk mel + encoder); one pooler per wave."""
+        ws = [np.ascontiguousarray(w, dtype=np.float32) for w in waves]
+        n = np.asarray([w.size for w in ws], np.int64)
+        flat = np.ascontiguousarray(np.concatenate(ws))
+        t_exp = [conv_len(conv_len(conv_len(1 + int(k) // 160))) for k in n]
+        out = np.empty((sum(t_exp), PROJ), np.float32)
+        t_out = np.zeros(len(ws), np.int32)
+        _check(lib().bark_hip_encode_wave_batch(self._h, _ptr(flat), _ptr(n), len(ws), _ptr(t_out), _ptr(out),
+                                                out.size))
+        res, row = [], 0
+        for t in t_out:
+            res.append(out[row : row + int(t)])
+            row += int(t)
+        return res
 
     def profile(self, enable: bool = True) -> None:
         """Per-operator HIP-event timing of the forward (BARK3_ENC_PROFILE)."""

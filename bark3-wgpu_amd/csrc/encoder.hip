@@ -885,6 +885,32 @@ struct BarkHip {
     if (!out_on_device) BARK_HIP_CHECK(hipStreamSynchronize(st));
   }
 
+  // log-mel of each wave (packed frames), then one batched encode
+  void encode_wave_batch(const float* waves, const int64_t* n_samples, int batch, int32_t* t_out, float* out,
+                         size_t cap) {
+    BARK_REQUIRE(batch >= 1 && waves && n_samples, "batch must be >= 1");
+    std::vector<int32_t> frames(batch), valid(batch);
+    size_t total_samples = 0, total_frames = 0;
+    for (int i = 0; i < batch; ++i) {
+      BARK_REQUIRE(n_samples[i] > 0, "empty wave");
+      total_samples += (size_t)n_samples[i];
+      frames[i] = mel_frames(n_samples[i]);
+      total_frames += (size_t)frames[i];
+    }
+    hipStream_t st = stream;
+    ensure(mel_wave, total_samples * 4);
+    ensure(mel, total_frames * MEL * 4);
+    BARK_HIP_CHECK(hipMemcpyAsync(mel_wave.p, waves, total_samples * 4, hipMemcpyHostToDevice, st));
+    size_t soff = 0, foff = 0;
+    for (int i = 0; i < batch; ++i) {
+      run_mel(mel_wave.as<float>() + soff, (long)n_samples[i], mel.as<float>() + foff * MEL, (size_t)frames[i] * MEL,
+              &frames[i], &valid[i], st);
+      soff += (size_t)n_samples[i];
+      foff += (size_t)frames[i];
+    }
+    encode_mel_batch(mel.as<float>(), true, frames.data(), valid.data(), batch, t_out, out, false, cap, st);
+  }
+
   void encode_sub(const float* sub_rows, int t, int dump_layer, float* out_pooler,
                   float* out_block) {
     BARK_REQUIRE(finalized, "encode before finalize");
@@ -1143,6 +1169,16 @@ int bark_hip_mel_device(BarkHip* h, const float* d_wave, int64_t n_samples, floa
     BARK_HIP_CHECK(hipSetDevice(h->device));
     hipStream_t st = stream ? static_cast<hipStream_t>(stream) : h->stream;
     h->run_mel(d_wave, (long)n_samples, d_features, cap, n_frames, n_valid, st);
+  });
+}
+
+int bark_hip_encode_wave_batch(BarkHip* h, const float* waves, const int64_t* n_samples, int32_t batch,
+                               int32_t* t_out, float* pooler, size_t pooler_cap) {
+  return guarded([&] {
+    BARK_REQUIRE(h && waves && n_samples && pooler, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    h->encode_wave_batch(waves, n_samples, batch, t_out, pooler, pooler_cap);
   });
 }
 

@@ -148,6 +148,15 @@ int bark_hip_mel(BarkHip *h, const float *wave, int64_t n_samples, float *featur
  * not synchronised; the output can feed bark_hip_encode_mel_batch_device. */
 int bark_hip_mel_device(BarkHip *h, const float *d_wave, int64_t n_samples, float *d_features, size_t cap,
                         int32_t *n_frames, int32_t *n_valid, void *stream);
+/* Batched chunk encode: the log-mel features (as bark_hip_mel) of each of
+ * `batch` 16 kHz waves, concatenated in `waves` with n_samples[i] samples
+ * each, encoded by one bark_hip_encode_mel_batch call — the per-chunk mel and
+ * encoder work of the reference's chunked transcription (src/inference.rs:
+ * 298-386, src/transcription.rs:56-122) as one batched call; each result equals
+ * that wave's own bark_hip_mel + bark_hip_encode_mel. pooler receives
+ * sum(t_out[i]) rows x 640 f32. Host buffers; synchronises. */
+int bark_hip_encode_wave_batch(BarkHip *h, const float *waves, const int64_t *n_samples, int32_t batch,
+                               int32_t *t_out, float *pooler, size_t pooler_cap);
 
 #ifdef __cplusplus
 }

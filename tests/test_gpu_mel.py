@@ -75,3 +75,23 @@ def test_mel_device_long_utterance(fe, filters):
     # FFT such as the reference's reaches ~1.4e-4 here against this f64 oracle)
     assert err.max() <= TOL
     assert np.quantile(err, 0.999) <= 1e-4
+
+
+def test_encode_wave_batch_equals_individual(pkg, synth, filters):
+    """bark_hip_encode_wave_batch = each wave's own mel + encode_mel, exactly
+    (chunked transcription as one batched call)."""
+    rng = np.random.default_rng(11)
+    lens = [14400 + 37, 36800 + 5, 24000]
+    print(f"case wave batch lens={lens}", flush=True)
+    waves = [(0.1 * rng.standard_normal(n)).astype(np.float32) for n in lens]
+    src = synth.SynthCheckpoint(seed=11, n_layers=2, style="rich", lowbit=True)
+    with pkg.HipEncoder.load_with(src, n_layers=2) as enc:
+        enc.set_mel_filters(filters)
+        batch = enc.encode_wave_batch(waves)
+        singles = []
+        for w in waves:
+            feats, nf, nv = enc.mel(w)
+            singles.append(enc.encode_mel(feats, nv)[0])
+    for b, s in zip(batch, singles):
+        assert b.shape == s.shape
+        assert np.array_equal(b, s)
