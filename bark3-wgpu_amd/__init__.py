@@ -152,6 +152,14 @@ _SIGS = {
         _c.c_int,
         [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_void_p, _c.c_size_t],
     ),
+    "bark_hip_tdt_decode": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_size_t, _c.POINTER(_c.c_int32)],
+    ),
+    "bark_hip_tdt_decode_device": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_size_t, _c.POINTER(_c.c_int32), _c.c_void_p],
+    ),
     "bark_hip_profile": (_c.c_int, [_c.c_void_p, _c.c_int]),
     "bark_hip_profile_only": (_c.c_int, [_c.c_void_p, _c.c_char_p]),
     "bark_hip_profile_report": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_size_t]),
@@ -216,6 +224,19 @@ def tensor_names(n_layers: int = LAYERS, front_end: bool = True) -> list[str]:
     return names
 
 
+# The greedy TDT decoder's tensors and shapes (TdtDecoder::from_source,
+# src/tdt.rs:130-162).
+TDT_SHAPES = {
+    "decoder.embedding.weight": (8193, 640),
+    "decoder.lstm.weight_ih_l0": (2560, 640), "decoder.lstm.weight_ih_l1": (2560, 640),
+    "decoder.lstm.weight_hh_l0": (2560, 640), "decoder.lstm.weight_hh_l1": (2560, 640),
+    "decoder.lstm.bias_ih_l0": (2560,), "decoder.lstm.bias_ih_l1": (2560,),
+    "decoder.lstm.bias_hh_l0": (2560,), "decoder.lstm.bias_hh_l1": (2560,),
+    "decoder.decoder_projector.weight": (640, 640), "decoder.decoder_projector.bias": (640,),
+    "joint.head.weight": (8198, 640), "joint.head.bias": (8198,),
+}
+
+
 class HipEncoder:
     """The HIP encoder on one device (Encoder, src/encoder.rs:89-139,412-830)."""
 
@@ -254,13 +275,18 @@ class HipEncoder:
         self.finalized = True
 
     @classmethod
-    def load_with(cls, src, device: int = 0, n_layers: int = LAYERS, front_end: bool = True) -> "HipEncoder":
+    def load_with(cls, src, device: int = 0, n_layers: int = LAYERS, front_end: bool = True,
+                  decoder=None) -> "HipEncoder":
         """Read every encoder tensor from `src` (read / read_lowbit, like the
-        reference's WeightSource) and upload it."""
+        reference's WeightSource) and upload it; with `decoder` (a source of
+        the TDT_SHAPES tensors), the greedy TDT decoder's weights too."""
         enc = cls(device, n_layers)
         for name in tensor_names(n_layers, front_end):
             low = src.read_lowbit(name) if hasattr(src, "read_lowbit") else None
             enc.set_tensor(name, low if low is not None else src.read(name))
+        if decoder is not None:
+            for name in TDT_SHAPES:
+                enc.set_tensor(name, decoder.read(name))
         enc.finalize()
         return enc
 
@@ -380,6 +406,32 @@ class HipEncoder:
             res.append(out[row : row + int(t)])
             row += int(t)
         return res
+
+    def tdt_decode(self, pooler: np.ndarray) -> np.ndarray:
+        """TdtDecoder::decode (src/tdt.rs:318): greedy TDT tokens of a pooler
+        (T, 640) as an (n, 3) u32 array of {id, frame, dur}."""
+        p = np.ascontiguousarray(pooler, dtype=np.float32)
+        if p.ndim != 2 or p.shape[1] != PROJ:
+            raise ValueError("pooler must be (T, 640)")
+        t = p.shape[0]
+        cap = t * 14 + 64
+        out = np.zeros((cap, 3), np.uint32)
+        n = ctypes.c_int32()
+        _check(lib().bark_hip_tdt_decode(self._h, _ptr(p) if t else None, t, _ptr(out), cap, ctypes.byref(n)))
+        return out[: n.value].copy()
+
+    def tdt_decode_device(self, d_pooler: int, t_len: int, stream: int = 0) -> np.ndarray:
+        """The same on a device pooler pointer (GpuTdtDecoder::decode_async)."""
+        cap = t_len * 14 + 64
+        out = np.zeros((cap, 3), np.uint32)
+        n = ctypes.c_int32()
+        _check(
+            lib().bark_hip_tdt_decode_device(
+                self._h, ctypes.c_void_p(d_pooler), int(t_len), _ptr(out), cap, ctypes.byref(n),
+                ctypes.c_void_p(stream) if stream else None,
+            )
+        )
+        return out[: n.value].copy()
 
     def profile(self, enable: bool = True) -> None:
         """Per-operator HIP-event timing of the forward (BARK3_ENC_PROFILE)."""

@@ -221,6 +221,13 @@ struct BarkHip {
   DevBuf mel_window, mel_twid, mel_rows, mel_vals, mel_ws, mel_wave, mel_feat;
   bool has_mel = false;
 
+  // greedy TDT decoder: weights (uploaded by finalize when the decoder's
+  // tensors were staged), state, and a pinned copy of the state words
+  TdtDev tdt;
+  bool has_tdt = false;
+  DevBuf tdt_state, tdt_h, tdt_c, tdt_dec, tdt_part, tdt_tokens, tdt_pooler;
+  int* tdt_host = nullptr;
+
   void set_mel_filters(const float* filters) {
     constexpr int NB = 257;
     std::vector<float> win(512, 0.0f);
@@ -317,9 +324,11 @@ struct BarkHip {
     DevBuf* bufs[] = {&pos, &sub16, &xn, &hid, &qu, &qv, &kh, &vt, &rk, &ao, &h, &h2, &glu, &part,
                       &pooler, &dump, &bounds, &tiles, &y2, &y3, &y4, &mel, &subf32,
                       &merges, &attn_lanes, &attn_po, &attn_pml, &mel_window, &mel_twid,
-                      &mel_rows, &mel_vals, &mel_ws, &mel_wave, &mel_feat};
+                      &mel_rows, &mel_vals, &mel_ws, &mel_wave, &mel_feat, &tdt_state, &tdt_h,
+                      &tdt_c, &tdt_dec, &tdt_part, &tdt_tokens, &tdt_pooler};
     for (DevBuf* b : bufs)
       if (b->p) (void)hipFree(b->p);
+    if (tdt_host) (void)hipHostFree(tdt_host);
     if (stream) (void)hipStreamDestroy(stream);
   }
 
@@ -498,8 +507,97 @@ struct BarkHip {
       sub_pw2 = to_device(linear(s + "6.weight", 256, 256, false));
       l6b = f32_dev(s + "6.bias", 256);
     }
+    has_tdt = staged.count("decoder.embedding.weight") > 0;
+    if (has_tdt) finalize_tdt();
     staged.clear();
     finalized = true;
+  }
+
+  // TdtDecoder::from_source (src/tdt.rs:130-162): embedding f32, LSTM /
+  // projection / head weights rounded to f16 (pack16), layer 0 and 1 joined.
+  void finalize_tdt() {
+    constexpr int DH = 640, GS = 4 * DH, NV = 8193, NR = 8198;
+    tdt.embed = f32_dev("decoder.embedding.weight", (int64_t)NV * DH);
+    auto joined16 = [&](const std::string& a, const std::string& b) {
+      HostLinear la = linear(a, GS, DH, false), lb = linear(b, GS, DH, false);
+      la.w16.insert(la.w16.end(), lb.w16.begin(), lb.w16.end());
+      return reinterpret_cast<const half*>(upload(la.w16.data(), la.w16.size()));
+    };
+    auto joined32 = [&](const std::string& a, const std::string& b) {
+      auto va = vec_f32(a, GS), vb = vec_f32(b, GS);
+      va.insert(va.end(), vb.begin(), vb.end());
+      return upload(va.data(), va.size());
+    };
+    const std::string d = "decoder.lstm.";
+    tdt.w_ih = joined16(d + "weight_ih_l0", d + "weight_ih_l1");
+    tdt.w_hh = joined16(d + "weight_hh_l0", d + "weight_hh_l1");
+    tdt.b_ih = joined32(d + "bias_ih_l0", d + "bias_ih_l1");
+    tdt.b_hh = joined32(d + "bias_hh_l0", d + "bias_hh_l1");
+    HostLinear pw = linear("decoder.decoder_projector.weight", DH, DH, false);
+    tdt.proj_w = reinterpret_cast<const half*>(upload(pw.w16.data(), pw.w16.size()));
+    tdt.proj_b = f32_dev("decoder.decoder_projector.bias", DH);
+    HostLinear hw = linear("joint.head.weight", NR, DH, false);
+    tdt.head_w = reinterpret_cast<const half*>(upload(hw.w16.data(), hw.w16.size()));
+    tdt.head_b = f32_dev("joint.head.bias", NR);
+    ensure(tdt_state, (size_t)tdt_state_words() * 4);
+    ensure(tdt_h, 4 * DH * 4);
+    ensure(tdt_c, 2 * DH * 4);
+    ensure(tdt_dec, DH * 4);
+    ensure(tdt_part, TDT_PARTIALS * 16);
+    BARK_HIP_CHECK(hipHostMalloc((void**)&tdt_host, (size_t)tdt_state_words() * 4, hipHostMallocDefault));
+    tdt.state = tdt_state.as<int>();
+    tdt.h = tdt_h.as<float>();
+    tdt.c = tdt_c.as<float>();
+    tdt.dec = tdt_dec.as<float>();
+    tdt.partials = tdt_part.as<float>();
+  }
+
+  // Greedy TDT decoding of a device pooler (t_len x 640 f32) on `st`
+  // (TdtDecoder::decode, src/tdt.rs:318-414; GpuTdtDecoder::decode_async,
+  // src/tdt_gpu.rs:206-300). Steps are queued in chunks; after each chunk only
+  // the state words come back, and decoding ends when the device sets `done`.
+  // Returns the number of tokens; their {id, frame, dur} words stay in
+  // tdt_tokens.
+  int tdt_decode(const float* d_pooler, int t_len, hipStream_t st) {
+    BARK_REQUIRE(finalized, "decode before finalize");
+    BARK_REQUIRE(has_tdt, "no TDT decoder tensors were set before finalize");
+    BARK_REQUIRE(t_len >= 0 && t_len <= (1 << 24), "t_len out of range");
+    if (t_len == 0) return 0;  // src/tdt_gpu.rs:211-216
+    const int max_steps = tdt_max_steps(t_len);
+    ensure(tdt_tokens, (size_t)max_steps * 12);
+    TdtDev d = tdt;
+    d.tokens = tdt_tokens.as<uint32_t>();
+    // per token step: joint head, both LSTM layers and the projection (f16)
+    const double step_bytes = 2.0 * 640 * (8198 + 4 * 2560 + 640);
+    const size_t words = (size_t)tdt_state_words() * 4;
+    tdt_begin(d, t_len, max_steps, st);
+    int steps = 0, chunk = std::max(16, t_len / 2);
+    while (true) {
+      const int n = std::min(chunk, max_steps - steps);
+      prof.run("tdt_decode", 0, step_bytes * n, st, [&] { tdt_steps(d, d_pooler, n, st); });
+      steps += n;
+      BARK_HIP_CHECK(hipMemcpyAsync(tdt_host, d.state, words, hipMemcpyDeviceToHost, st));
+      BARK_HIP_CHECK(hipStreamSynchronize(st));
+      if (tdt_host[tdt_done_word()] || steps >= max_steps) break;
+      // the rest at the rate seen so far (steps per frame), plus a margin
+      const int frame = tdt_host[tdt_frame_word()];
+      const double rate = (double)steps / std::max(frame, 1);
+      chunk = std::max(16, (int)(rate * (t_len - frame)) + 8);
+    }
+    BARK_REQUIRE(tdt_host[tdt_done_word()], "TDT decoding did not finish within the step guard");
+    return tdt_host[tdt_count_word()];
+  }
+
+  void tdt_decode_copy(const float* d_pooler, int t_len, uint32_t* tokens, size_t cap, int32_t* n_tokens,
+                       hipStream_t st) {
+    const int n = tdt_decode(d_pooler, t_len, st);
+    if (n_tokens) *n_tokens = n;
+    BARK_REQUIRE((size_t)n <= cap, "token buffer too small: " + std::to_string(n) + " tokens");
+    if (n > 0) {
+      BARK_REQUIRE(tokens, "null token buffer");
+      BARK_HIP_CHECK(hipMemcpyAsync(tokens, tdt_tokens.p, (size_t)n * 12, hipMemcpyDeviceToHost, st));
+      BARK_HIP_CHECK(hipStreamSynchronize(st));
+    }
   }
 
   // ------------------------------------------------------- position table --
@@ -1179,6 +1277,33 @@ int bark_hip_encode_wave_batch(BarkHip* h, const float* waves, const int64_t* n_
     std::lock_guard<std::mutex> lk(h->mu);
     BARK_HIP_CHECK(hipSetDevice(h->device));
     h->encode_wave_batch(waves, n_samples, batch, t_out, pooler, pooler_cap);
+  });
+}
+
+int bark_hip_tdt_decode(BarkHip* h, const float* pooler, int32_t t_len, uint32_t* tokens, size_t cap,
+                        int32_t* n_tokens) {
+  return guarded([&] {
+    BARK_REQUIRE(h && (pooler || t_len == 0), "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    BARK_REQUIRE(t_len >= 0 && t_len <= (1 << 24), "t_len out of range");
+    if (t_len > 0) {
+      h->ensure(h->tdt_pooler, (size_t)t_len * 640 * 4);
+      BARK_HIP_CHECK(hipMemcpyAsync(h->tdt_pooler.p, pooler, (size_t)t_len * 640 * 4, hipMemcpyHostToDevice,
+                                    h->stream));
+    }
+    h->tdt_decode_copy(h->tdt_pooler.as<float>(), t_len, tokens, cap, n_tokens, h->stream);
+  });
+}
+
+int bark_hip_tdt_decode_device(BarkHip* h, const float* d_pooler, int32_t t_len, uint32_t* tokens, size_t cap,
+                               int32_t* n_tokens, void* stream) {
+  return guarded([&] {
+    BARK_REQUIRE(h && (d_pooler || t_len == 0), "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    hipStream_t st = stream ? static_cast<hipStream_t>(stream) : h->stream;
+    h->tdt_decode_copy(d_pooler, t_len, tokens, cap, n_tokens, st);
   });
 }
 

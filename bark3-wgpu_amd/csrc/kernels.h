@@ -166,4 +166,29 @@ size_t mel_workspace_bytes(long n_samples);   // scratch of mel_features
 void mel_features(const float* wave, long n_samples, const MelTables& tb, void* workspace, float* out,
                   hipStream_t st);
 
+// ---------------------------------------------------------------- TDT --
+// Device buffers of the greedy TDT decoder (tdt.hip): embedding (8193 x 640)
+// and biases f32; LSTM (2 layers x 2560 x 640, ih and hh), projection
+// (640 x 640) and joint head (8198 x 640) f16; state words; h (2 layers x 2
+// buffers x 640), c (2 x 640), dec (640), joint partials (256 float4),
+// tokens (cap x {id, frame, dur}).
+struct TdtDev {
+  const float* embed = nullptr;
+  const half *w_ih = nullptr, *w_hh = nullptr, *proj_w = nullptr, *head_w = nullptr;
+  const float *b_ih = nullptr, *b_hh = nullptr, *proj_b = nullptr, *head_b = nullptr;
+  int* state = nullptr;
+  float *h = nullptr, *c = nullptr, *dec = nullptr, *partials = nullptr;
+  uint32_t* tokens = nullptr;
+};
+constexpr int TDT_PARTIALS = 256;  // workgroups of a phase, one joint partial each
+int tdt_state_words();
+int tdt_frame_word();  // index of the frame pointer among the state words
+int tdt_done_word();   // index of the `done` flag
+int tdt_count_word();  // index of the emitted-token count
+int tdt_max_steps(int t_len);
+// reset the state for a pooler of t_len frames and run the start LSTM step
+void tdt_begin(const TdtDev& d, int t_len, int cap, hipStream_t st);
+// queue `steps` decode steps (steps after the end return at once)
+void tdt_steps(const TdtDev& d, const float* pooler, int steps, hipStream_t st);
+
 }  // namespace bark

@@ -166,3 +166,43 @@ def dequant(t) -> np.ndarray:
 def mel(frames: int, seed: int = 0) -> np.ndarray:
     """Synthetic log-mel features (frames, 128) ~ N(0, 1)."""
     return np.random.default_rng([seed, 7]).standard_normal((frames, 128), dtype=np.float32)
+
+
+class SynthTdt:
+    """Seeded TDT decoder weights under the reference's names (TDT_SHAPES).
+
+    LSTM and projection entries ~ U(-1/sqrt(640), 1/sqrt(640)) (torch's LSTM /
+    Linear initialisation), embedding N(0, 1), joint head N(0, 1/sqrt(640))
+    with biases N(0, 0.1), the blank row's bias raised by `blank_bias` and the
+    duration rows' by (dur0_bias, 0.5, 0.3, 0, -0.3), so that blanks, tokens and
+    every duration occur. A dur0_bias near -0.6 makes runs of duration-0
+    tokens that the step guard ends. Matrices hold f16-representable values
+    (the decoder keeps them as f16), vectors f32.
+    """
+
+    def __init__(self, seed: int = 0, blank_bias: float = 2.5, dur0_bias: float = -1.5):
+        self.seed, self.blank_bias, self.dur0_bias = seed, blank_bias, dur0_bias
+
+    def read(self, name: str) -> np.ndarray:
+        from . import TDT_SHAPES
+
+        shp = TDT_SHAPES[name]
+        rng = np.random.default_rng([self.seed, zlib.crc32(name.encode()), 5])
+        k = 1.0 / np.sqrt(640.0)
+        if name == "decoder.embedding.weight":
+            return rng.standard_normal(shp, dtype=np.float32)
+        if name.startswith("decoder."):
+            v = rng.uniform(-k, k, shp).astype(np.float32)
+        elif name == "joint.head.weight":
+            v = (rng.standard_normal(shp, dtype=np.float32) * k).astype(np.float32)
+        else:
+            v = rng.standard_normal(shp, dtype=np.float32) * np.float32(0.1)
+            if name == "joint.head.bias":
+                v[8192] += np.float32(self.blank_bias)
+                v[8193:] += np.asarray((self.dur0_bias, 0.5, 0.3, 0.0, -0.3), np.float32)
+        return v.astype(np.float16).astype(np.float32) if len(shp) == 2 else v
+
+
+def pooler(t: int, seed: int = 0) -> np.ndarray:
+    """Synthetic encoder output (t, 640) ~ N(0, 1)."""
+    return np.random.default_rng([seed, 11]).standard_normal((t, 640), dtype=np.float32)

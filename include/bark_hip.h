@@ -106,6 +106,31 @@ int bark_hip_encode_mel_batch_device(BarkHip *h, const float *d_mel, const int32
                                      const int32_t *n_valid, int32_t batch, int32_t *t_out,
                                      float *d_pooler, size_t pooler_cap, void *stream);
 
+/* ---- TDT decoder ---------------------------------------------------------
+ * Present when the decoder's tensors were set before bark_hip_finalize, under
+ * the reference's names (TdtDecoder::from_source, src/tdt.rs:130-162):
+ * "decoder.embedding.weight" (8193, 640), "decoder.lstm.weight_ih_l0/_l1",
+ * "decoder.lstm.weight_hh_l0/_l1" (2560, 640), "decoder.lstm.bias_ih_l0/_l1",
+ * "decoder.lstm.bias_hh_l0/_l1" (2560), "decoder.decoder_projector.weight"
+ * (640, 640) and ".bias", "joint.head.weight" (8198, 640) and ".bias". Matrices
+ * are kept as f16 (RNE) like the reference's pack16. */
+
+/* TdtDecoder::decode (src/tdt.rs:318-414): greedy TDT decoding of a host
+ * pooler (t_len, 640) f32. tokens receives n_tokens {id, frame, dur} u32
+ * triples (tdt::Token, src/tdt.rs:31-41); cap counts triples, and a count above
+ * it is an error (BARK_HIP_EINVAL, n_tokens still set). t_len * 14 + 64
+ * triples always suffice. t_len == 0 gives no tokens. */
+int bark_hip_tdt_decode(BarkHip *h, const float *pooler, int32_t t_len, uint32_t *tokens, size_t cap,
+                        int32_t *n_tokens);
+
+/* GpuTdtDecoder::decode_async (src/tdt_gpu.rs:206-300): the same on a device
+ * pooler (e.g. the output of bark_hip_encode_mel_batch_device), queued on
+ * `stream` (NULL = the handle's stream). The decoder state stays on the device;
+ * the call synchronises once per chunk of steps and returns with the tokens
+ * in host memory. */
+int bark_hip_tdt_decode_device(BarkHip *h, const float *d_pooler, int32_t t_len, uint32_t *tokens,
+                               size_t cap, int32_t *n_tokens, void *stream);
+
 /* Per-operator GPU timing, the counterpart of BARK3_ENC_PROFILE
  * (src/encoder/prof.rs:1-127, src/encoder.rs:823-827): while enabled, every
  * launch of the forward is bracketed by HIP events on its stream. Enabling or

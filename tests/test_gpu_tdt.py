@@ -1,0 +1,135 @@
+"""GPU parity of the greedy TDT decoder (TdtDecoder::decode, src/tdt.rs:318-414;
+GpuTdtDecoder::decode_async, src/tdt_gpu.rs:206-300) through the C ABI
+(bark_hip_tdt_decode / bark_hip_tdt_decode_device): tokens {id, frame, dur}
+equal to the transformers fixture and to the oracle, including duration-0
+runs, the step guard, one-frame and empty poolers, and the device-resident
+pooler of the encoder. Every case's smallest decision margin in the oracle
+(best minus runner-up score) is checked to exceed the GPU's f32 rounding, so
+equality is the expected outcome, not luck."""
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import tdt as otdt
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+GOLD = Path(__file__).resolve().parent / "golden" / "tdt_fixture.npz"
+MIN_MARGIN = 1e-5  # f32 dot products of 640 terms and the LSTM state differ from f64 by ~1e-6
+
+
+def make(pkg, synth, **kw):
+    enc = pkg.HipEncoder.load_with(synth.SynthCheckpoint(seed=1, n_layers=1), 0, 1, decoder=synth.SynthTdt(**kw))
+    return enc
+
+
+@pytest.fixture(scope="module")
+def base(pkg, synth):
+    enc = make(pkg, synth, seed=0)
+    yield enc
+    enc.close()
+
+
+def oracle(synth, kw, frames, pseed):
+    toks, margins = otdt.Decoder(synth.SynthTdt(**kw)).decode(synth.pooler(frames, pseed), with_margins=True)
+    assert margins.min() > MIN_MARGIN
+    return toks
+
+
+@pytest.mark.parametrize("case,frames,pseed", [("base", 300, 0), ("short", 7, 3)])
+def test_tdt_vs_fixture(base, synth, case, frames, pseed):
+    print(f"case tdt fixture {case}", flush=True)
+    gold = np.load(GOLD, allow_pickle=False)
+    np.testing.assert_array_equal(base.tdt_decode(synth.pooler(frames, pseed)), gold[f"{case}_tokens"])
+
+
+@pytest.mark.parametrize("frames,pseed", [(1000, 2), (300, 1), (1, 4), (2, 5)])
+def test_tdt_vs_oracle(base, synth, frames, pseed):
+    print(f"case tdt oracle T={frames} seed={pseed}", flush=True)
+    np.testing.assert_array_equal(base.tdt_decode(synth.pooler(frames, pseed)), oracle(synth, {"seed": 0}, frames, pseed))
+
+
+def test_tdt_empty(base):
+    print("case tdt empty", flush=True)
+    assert base.tdt_decode(np.zeros((0, 640), np.float32)).shape == (0, 3)
+
+
+def test_tdt_duration0_and_guard(pkg, synth):
+    """duration-0 tokens (fixture), then a run of them that the step guard ends"""
+    print("case tdt dur0 fixture", flush=True)
+    gold = np.load(GOLD, allow_pickle=False)
+    enc = make(pkg, synth, seed=0, dur0_bias=-0.8)
+    try:
+        np.testing.assert_array_equal(enc.tdt_decode(synth.pooler(300, 0)), gold["dur0_tokens"])
+    finally:
+        enc.close()
+    print("case tdt guard", flush=True)
+    enc = make(pkg, synth, seed=0, dur0_bias=-0.6)
+    try:
+        got = enc.tdt_decode(synth.pooler(100, 0))
+        want = oracle(synth, {"seed": 0, "dur0_bias": -0.6}, 100, 0)
+        assert len(want) > 1000
+        np.testing.assert_array_equal(got, want)
+    finally:
+        enc.close()
+
+
+def test_tdt_cap_too_small(pkg, base, synth):
+    import ctypes
+
+    print("case tdt cap", flush=True)
+    p = np.ascontiguousarray(synth.pooler(300, 0))
+    out = np.zeros((4, 3), np.uint32)
+    n = ctypes.c_int32()
+    rc = pkg.lib().bark_hip_tdt_decode(base._h, p.ctypes.data, 300, out.ctypes.data, 4, ctypes.byref(n))
+    assert rc != 0 and n.value == 84
+    assert b"token buffer too small" in pkg.lib().bark_hip_last_error()
+
+
+def test_tdt_device_pooler(base, synth):
+    """a pooler already in device memory (torch tensor), on torch's stream"""
+    print("case tdt device", flush=True)
+    p = synth.pooler(1000, 2)
+    d = torch.from_numpy(p).to("cuda:0")
+    s = torch.cuda.current_stream().cuda_stream
+    got = base.tdt_decode_device(d.data_ptr(), 1000, s)
+    np.testing.assert_array_equal(got, base.tdt_decode(p))
+
+
+def test_tdt_after_encoder(pkg, synth):
+    """the encoder's device-resident pooler decoded in place equals decoding
+    the host copy of the same pooler (the synthetic encoder's small outputs
+    leave the decision to the decoder state, so the blank bias is lowered to
+    make tokens occur)"""
+    print("case tdt after encoder", flush=True)
+    enc = make(pkg, synth, seed=0, blank_bias=-1.0)
+    try:
+        mel = synth.mel(2000, 3)
+        pooler, t = enc.encode_mel(mel)
+        host = enc.tdt_decode(pooler)
+        dm = torch.from_numpy(np.ascontiguousarray(mel)).to("cuda:0")
+        dp = torch.empty((t, 640), dtype=torch.float32, device="cuda:0")
+        s = torch.cuda.current_stream().cuda_stream
+        n = [mel.shape[0]]
+        t_out = enc.encode_mel_batch_device(dm.data_ptr(), n, n, dp.data_ptr(), dp.numel(), s)
+        assert list(t_out) == [t]
+        np.testing.assert_array_equal(enc.tdt_decode_device(dp.data_ptr(), t, s), host)
+        assert len(host) > 0
+    finally:
+        enc.close()
+
+
+
+def test_tdt_repeat_after_other_lengths(base, synth):
+    """the state is reset per call: a decode after longer and shorter ones
+    gives the same tokens"""
+    print("case tdt repeat", flush=True)
+    p = synth.pooler(300, 1)
+    first = base.tdt_decode(p)
+    base.tdt_decode(synth.pooler(1000, 2))
+    base.tdt_decode(synth.pooler(1, 4))
+    np.testing.assert_array_equal(base.tdt_decode(p), first)
