@@ -539,7 +539,7 @@ struct BarkHip {
     HostLinear hw = linear("joint.head.weight", NR, DH, false);
     tdt.head_w = reinterpret_cast<const half*>(upload(hw.w16.data(), hw.w16.size()));
     tdt.head_b = f32_dev("joint.head.bias", NR);
-    ensure(tdt_state, (size_t)tdt_state_words() * 4);
+    ensure(tdt_state, (size_t)tdt_state_words() * 2 * 4);  // current and next control state
     ensure(tdt_h, 4 * DH * 4);
     ensure(tdt_c, 2 * DH * 4);
     ensure(tdt_dec, DH * 4);

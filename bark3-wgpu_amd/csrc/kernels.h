@@ -169,7 +169,8 @@ void mel_features(const float* wave, long n_samples, const MelTables& tb, void* 
 // ---------------------------------------------------------------- TDT --
 // Device buffers of the greedy TDT decoder (tdt.hip): embedding (8193 x 640)
 // and biases f32; LSTM (2 layers x 2560 x 640, ih and hh), projection
-// (640 x 640) and joint head (8198 x 640) f16; state words; h (2 layers x 2
+// (640 x 640) and joint head (8198 x 640) f16; state words (the current
+// control state, then the next one); h (2 layers x 2
 // buffers x 640), c (2 x 640), dec (640), joint partials (256 float4),
 // tokens (cap x {id, frame, dur}).
 struct TdtDev {
@@ -181,7 +182,7 @@ struct TdtDev {
   uint32_t* tokens = nullptr;
 };
 constexpr int TDT_PARTIALS = 256;  // workgroups of a phase, one joint partial each
-int tdt_state_words();
+int tdt_state_words();  // words of one control state (the buffer holds two)
 int tdt_frame_word();  // index of the frame pointer among the state words
 int tdt_done_word();   // index of the `done` flag
 int tdt_count_word();  // index of the emitted-token count

@@ -3,25 +3,30 @@
 // emitted tokens kept in device memory, as GpuTdtDecoder does
 // (src/tdt_gpu.rs:1-7, 206-300).
 //
-// A decode step is five launches on one stream; each reads only what the
+// A decode step is four launches on one stream; each reads only what the
 // launches before it wrote, so kernel boundaries are the only synchronisation,
 // and the control state (frame, step count, parity of the h buffers, whether
 // the LSTM runs) lives in device memory:
 //   joint  x = relu(pooler[frame] + dec); scores of the 8198 head rows (8193
 //          tokens + 5 durations, f16 weights, f32 sums, src/tdt.rs:217-288)
 //          over G workgroups, each leaving its best token and best duration;
-//   decide one wave reduces the partials and applies the step: blank: frame +=
-//          max(dur, 1); token: record {id, frame, dur}, run the LSTM, frame +=
-//          dur (src/tdt.rs:386-412); `done` once the loop would exit (frame >=
-//          T or the step guard T * 14 + 64);
-//   lstm   (twice) one wave per channel: its i, f, g, o gate rows of w_ih and
-//          w_hh (8 row dots, 8 lanes each), gate = b_ih + b_hh + w_ih.x +
-//          w_hh.h_old, c = f c + i g, h = o tanh(c) (src/tdt.rs:179-214);
-//   proj   dec = b + W h1 (src/tdt.rs:515-529).
-// Launches after `done`, and lstm / proj after a blank, return at once. The
+//   lstm0  every workgroup reduces the partials to the step's decision (the
+//          same everywhere) and workgroup 0 applies it to the next control
+//          state: blank: frame += max(dur, 1); token: record {id, frame, dur},
+//          frame += dur (src/tdt.rs:386-412); `done` once the loop would exit
+//          (frame >= T or the step guard T * 14 + 64). For a token that does
+//          not end the decode, LSTM layer 0 on its embedding: one wave per
+//          channel holds its i, f, g, o gate rows of w_ih and w_hh (8 row
+//          dots, 8 lanes each), gate = b_ih + b_hh + w_ih.x + w_hh.h_old,
+//          c = f c + i g, h = o tanh(c) (src/tdt.rs:179-214);
+//   lstm1  layer 1 on the new h0;
+//   proj   dec = b + W h1 (src/tdt.rs:515-529); workgroup 0 makes the next
+//          control state the current one.
+// Launches after `done`, and lstm1 / proj after a blank, return at once. The
 // host queues steps in chunks and reads back only the state words. Row dots
 // read each 1280-byte f16 row with 8 lanes (ten 16-byte loads each, issued
-// before the input vector is staged in LDS, so both loads overlap).
+// before the input vector is staged in LDS or the decision is known, so the
+// loads overlap).
 //
 // Measured alternatives: deciding in the joint's last workgroup (an arrival
 // counter) and a single cooperative launch with grid barriers between the
@@ -42,7 +47,6 @@ namespace {
 constexpr int DH = 640, GS = 4 * DH;
 constexpr int VOCAB = 8193, NROWS = VOCAB + 5, BLANK = 8192;
 constexpr int WAVES = 8, THREADS = 64 * WAVES;
-constexpr int GROUPS = THREADS / 8;  // 8-lane row groups per workgroup
 constexpr int ROW_LOADS = DH / 8 / 8;  // 16-byte loads per lane per row (10)
 constexpr int NONE = 0x7fffffff;
 
@@ -173,36 +177,40 @@ __device__ inline float sigmoid_ref(float x) { return __fdiv_rn(1.0f, __fadd_rn(
 
 // one LSTM layer: input x, previous h (nullptr = zeros, and c = 0), new h into
 // h_new; c of the layer updated in place. Channel ch is owned by wave ch / G of
-// workgroup ch % G, the same owner every step.
-__device__ void phase_lstm(const Weights& W, int layer, const float* x, const float* h_old, float* h_new, float* c,
-                           int G, int wg, Lds& sh) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int ch = wg + G * wave;
-  const int grp = lane >> 3, sub = lane & 7;
-  const int kind = grp >> 1, hh = grp & 1;  // gate i, f, g, o; input or hidden weights
-  Row row;
-  if (ch < DH) row.load((hh ? W.w_hh : W.w_ih) + ((size_t)layer * GS + kind * DH + ch) * DH, sub);
+// workgroup ch % G, the same owner every step; lane group g of the wave holds
+// gate row g / 2 (i, f, g, o) of w_ih (g even) or w_hh (g odd), loaded by
+// lstm_row before the input is known.
+__device__ inline bool lstm_row(const Weights& W, int layer, int G, int wg, Row& row) {
+  const int lane = threadIdx.x & 63, ch = wg + G * (threadIdx.x >> 6);
+  if (ch >= DH) return false;
+  const int grp = lane >> 3;
+  row.load(((grp & 1) ? W.w_hh : W.w_ih) + ((size_t)layer * GS + (grp >> 1) * DH + ch) * DH, lane & 7);
+  return true;
+}
+
+__device__ void phase_lstm(const Weights& W, int layer, const Row& row, bool has_row, const float* x,
+                           const float* h_old, float* h_new, float* c, int G, int wg, Lds& sh) {
   for (int k = threadIdx.x; k < DH; k += THREADS) {
     sh.xs[k] = x[k];
     sh.hs[k] = h_old ? h_old[k] : 0.0f;
   }
   __syncthreads();
-  if (ch < DH) {
-    const float v = row.dot(hh ? sh.hs : sh.xs, sub);
-    float g4[4];
+  if (!has_row) return;
+  const int lane = threadIdx.x & 63, ch = wg + G * (threadIdx.x >> 6);
+  const float v = row.dot(((lane >> 3) & 1) ? sh.hs : sh.xs, lane & 7);
+  float g4[4];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float di = __shfl(v, 16 * k, 64), dh = __shfl(v, 16 * k + 8, 64);
-      const int rk = layer * GS + k * DH + ch;
-      g4[k] = ((W.b_ih[rk] + W.b_hh[rk]) + di) + dh;
-    }
-    if (lane == 0) {
-      const float ig = sigmoid_ref(g4[0]), fg = sigmoid_ref(g4[1]), gg = tanhf(g4[2]);
-      const float c_old = h_old ? c[ch] : 0.0f;
-      const float cn = __fadd_rn(__fmul_rn(fg, c_old), __fmul_rn(ig, gg));
-      c[ch] = cn;
-      h_new[ch] = __fmul_rn(sigmoid_ref(g4[3]), tanhf(cn));
-    }
+  for (int k = 0; k < 4; ++k) {
+    const float di = __shfl(v, 16 * k, 64), dh = __shfl(v, 16 * k + 8, 64);
+    const int rk = layer * GS + k * DH + ch;
+    g4[k] = ((W.b_ih[rk] + W.b_hh[rk]) + di) + dh;
+  }
+  if (lane == 0) {
+    const float ig = sigmoid_ref(g4[0]), fg = sigmoid_ref(g4[1]), gg = tanhf(g4[2]);
+    const float c_old = h_old ? c[ch] : 0.0f;
+    const float cn = __fadd_rn(__fmul_rn(fg, c_old), __fmul_rn(ig, gg));
+    c[ch] = cn;
+    h_new[ch] = __fmul_rn(sigmoid_ref(g4[3]), tanhf(cn));
   }
 }
 
@@ -229,74 +237,102 @@ __global__ void __launch_bounds__(THREADS) tdt_joint_kernel(Weights W, const flo
   phase_joint(W, pooler + (size_t)state[S_FRAME] * DH, dec, part, gridDim.x, blockIdx.x, sh);
 }
 
-// the step's decision: one wave reduces the joint partials and applies it
-__global__ void __launch_bounds__(64) tdt_decide_kernel(int* state, const float4* part, int G, uint32_t* tokens) {
-  if (state[S_DONE]) return;
+// Layer 0 of the LSTM, preceded by the step's decision: every workgroup
+// reduces the joint partials itself (the same result everywhere), and
+// workgroup 0 writes the updated control state to `next` (the words this
+// launch reads stay unchanged until the projection copies `next` back).
+// blank: frame += max(dur, 1); token: record {id, frame, dur}, frame += dur,
+// and the LSTM runs on its embedding unless decoding ends here. With `start`
+// set this is the start step on the blank embedding from h = c = 0.
+__global__ void __launch_bounds__(THREADS) tdt_lstm0_kernel(Weights W, int start, const int* state, int* next,
+                                                            const float4* part, uint32_t* tokens, float* h,
+                                                            float* c) {
+  if (!start && state[S_DONE]) return;
   __shared__ Lds sh;
-  phase_decide(part, G, sh);
-  if (threadIdx.x != 0) return;
-  const int tok = sh.tok, dur = sh.dur;
-  int frame = state[S_FRAME];
-  const int guard = state[S_GUARD] + 1;
-  state[S_GUARD] = guard;
-  int emit = 0;
-  if (tok == BLANK) {
-    frame += max(dur, 1);
-  } else {
-    const int n = state[S_NTOK];
-    if (n < state[S_CAP]) {
-      tokens[3 * n] = (uint32_t)tok;
-      tokens[3 * n + 1] = (uint32_t)frame;
-      tokens[3 * n + 2] = (uint32_t)dur;
+  const int G = gridDim.x, wg = blockIdx.x;
+  Row row;
+  const bool has_row = lstm_row(W, 0, G, wg, row);
+  int tok = BLANK, p = 0;
+  if (!start) {
+    phase_decide(part, TDT_PARTIALS, sh);
+    tok = sh.tok;
+    const int dur = sh.dur;
+    int frame = state[S_FRAME], ntok = state[S_NTOK], lstm = state[S_LSTM];
+    const int guard = state[S_GUARD] + 1;
+    const bool token = tok != BLANK;
+    if (token) {
+      if (wg == 0 && threadIdx.x == 0 && ntok < state[S_CAP]) {
+        tokens[3 * ntok] = (uint32_t)tok;
+        tokens[3 * ntok + 1] = (uint32_t)frame;
+        tokens[3 * ntok + 2] = (uint32_t)dur;
+      }
+      ++ntok;
+      frame += dur;
+    } else {
+      frame += max(dur, 1);
     }
-    state[S_NTOK] = n + 1;
-    frame += dur;
-    emit = 1;
+    const bool done = frame >= state[S_TLEN] || guard >= state[S_MAXSTEPS];
+    // the new decoder state is only needed if another step follows
+    const bool emit = token && !done;
+    p = lstm & 1;
+    if (wg == 0 && threadIdx.x < S_WORDS) {
+      int v = state[threadIdx.x];
+      switch (threadIdx.x) {
+        case S_FRAME: v = frame; break;
+        case S_DONE: v = done; break;
+        case S_NTOK: v = ntok; break;
+        case S_GUARD: v = guard; break;
+        case S_TOKEN: v = emit ? tok : v; break;
+        case S_EMIT: v = emit; break;
+        case S_PAR: v = emit ? p : v; break;
+        case S_LSTM: v = emit ? lstm + 1 : v; break;
+        default: break;
+      }
+      next[threadIdx.x] = v;
+    }
+    if (!emit) return;
   }
-  const int done = frame >= state[S_TLEN] || guard >= state[S_MAXSTEPS];
-  state[S_FRAME] = frame;
-  state[S_DONE] = done;
-  // the new decoder state is only needed if another step follows
-  state[S_EMIT] = emit && !done;
-  if (emit && !done) {
-    state[S_TOKEN] = tok;
-    state[S_PAR] = state[S_LSTM] & 1;
-    state[S_LSTM] += 1;
-  }
+  const bool first = start != 0;
+  phase_lstm(W, 0, row, has_row, W.embed + (size_t)tok * DH, first ? nullptr : h + (size_t)p * DH,
+             h + (size_t)(p ^ 1) * DH, c, G, wg, sh);
 }
 
-// h[layer][S_PAR] holds the old state, h[layer][S_PAR ^ 1] receives the new one
-__global__ void __launch_bounds__(THREADS) tdt_lstm_kernel(Weights W, int layer, const int* state, float* h,
-                                                           float* c) {
-  if (!state[S_EMIT]) return;
+// layer 1: h[1][S_PAR] holds the old state, h[1][S_PAR ^ 1] receives the new
+// one; the input is the new h0 = h[0][S_PAR ^ 1]
+__global__ void __launch_bounds__(THREADS) tdt_lstm1_kernel(Weights W, const int* next, float* h, float* c) {
+  if (!next[S_EMIT]) return;
   __shared__ Lds sh;
-  const int p = state[S_PAR];
-  const bool first = state[S_LSTM] == 1;  // the start step: h = c = 0
-  const float* x = layer == 0 ? W.embed + (size_t)state[S_TOKEN] * DH : h + (size_t)(p ^ 1) * DH;
-  phase_lstm(W, layer, x, first ? nullptr : h + (size_t)(layer * 2 + p) * DH, h + (size_t)(layer * 2 + (p ^ 1)) * DH,
-             c + (size_t)layer * DH, gridDim.x, blockIdx.x, sh);
+  Row row;
+  const bool has_row = lstm_row(W, 1, gridDim.x, blockIdx.x, row);
+  const int p = next[S_PAR];
+  const bool first = next[S_LSTM] == 1;  // the start step: h = c = 0
+  phase_lstm(W, 1, row, has_row, h + (size_t)(p ^ 1) * DH, first ? nullptr : h + (size_t)(2 + p) * DH,
+             h + (size_t)(2 + (p ^ 1)) * DH, c + DH, gridDim.x, blockIdx.x, sh);
 }
 
-__global__ void __launch_bounds__(THREADS) tdt_proj_kernel(Weights W, const int* state, const float* h,
+// dec = b + W h1_new, then workgroup 0 makes `next` the current state
+__global__ void __launch_bounds__(THREADS) tdt_proj_kernel(Weights W, int* state, const int* next, const float* h,
                                                            float* dec) {
-  if (!state[S_EMIT]) return;
   __shared__ Lds sh;
-  phase_proj(W, h + (size_t)(2 + (state[S_PAR] ^ 1)) * DH, dec, gridDim.x, blockIdx.x, sh);
+  if (next[S_EMIT]) phase_proj(W, h + (size_t)(2 + (next[S_PAR] ^ 1)) * DH, dec, gridDim.x, blockIdx.x, sh);
+  if (blockIdx.x == 0 && threadIdx.x < S_WORDS) state[threadIdx.x] = next[threadIdx.x];
 }
 
+// both state copies: frame 0, the start step pending (blank, parity 0)
 __global__ void tdt_init_kernel(int* state, int t_len, int max_steps, int cap) {
-  if (threadIdx.x == 0) {
-    state[S_FRAME] = 0;
-    state[S_DONE] = t_len <= 0;
-    state[S_NTOK] = 0;
-    state[S_GUARD] = 0;
-    state[S_TOKEN] = BLANK;
-    state[S_EMIT] = 1;
-    state[S_PAR] = 0;
-    state[S_LSTM] = 1;
-    state[S_TLEN] = t_len;
-    state[S_MAXSTEPS] = max_steps;
-    state[S_CAP] = cap;
+  if (threadIdx.x < 2) {
+    int* s = state + threadIdx.x * S_WORDS;
+    s[S_FRAME] = 0;
+    s[S_DONE] = t_len <= 0;
+    s[S_NTOK] = 0;
+    s[S_GUARD] = 0;
+    s[S_TOKEN] = BLANK;
+    s[S_EMIT] = 1;
+    s[S_PAR] = 0;
+    s[S_LSTM] = 1;
+    s[S_TLEN] = t_len;
+    s[S_MAXSTEPS] = max_steps;
+    s[S_CAP] = cap;
   }
 }
 
@@ -316,23 +352,28 @@ int tdt_max_steps(int t_len) { return t_len * (10 + 4) + 64; }  // src/tdt.rs:38
 
 void tdt_begin(const TdtDev& d, int t_len, int cap, hipStream_t st) {
   const Weights W = weights_of(d);
+  int* next = d.state + S_WORDS;
+  const float4* part = reinterpret_cast<const float4*>(d.partials);
   BARK_LAUNCH(tdt_init_kernel, dim3(1), dim3(64), 0, st, d.state, t_len, tdt_max_steps(t_len), cap);
-  for (int layer = 0; layer < 2; ++layer)
-    BARK_LAUNCH(tdt_lstm_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, layer, (const int*)d.state, d.h, d.c);
-  BARK_LAUNCH(tdt_proj_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, (const int*)d.state, (const float*)d.h, d.dec);
+  BARK_LAUNCH(tdt_lstm0_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, 1, (const int*)d.state, next, part, d.tokens,
+              d.h, d.c);
+  BARK_LAUNCH(tdt_lstm1_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, (const int*)next, d.h, d.c);
+  BARK_LAUNCH(tdt_proj_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, d.state, (const int*)next, (const float*)d.h,
+              d.dec);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
 void tdt_steps(const TdtDev& d, const float* pooler, int steps, hipStream_t st) {
   const Weights W = weights_of(d);
+  int* next = d.state + S_WORDS;
   float4* part = reinterpret_cast<float4*>(d.partials);
   for (int s = 0; s < steps; ++s) {
     BARK_LAUNCH(tdt_joint_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, pooler, (const float*)d.dec,
                 (const int*)d.state, part);
-    BARK_LAUNCH(tdt_decide_kernel, dim3(1), dim3(64), 0, st, d.state, (const float4*)part, STEP_G, d.tokens);
-    for (int layer = 0; layer < 2; ++layer)
-      BARK_LAUNCH(tdt_lstm_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, layer, (const int*)d.state, d.h, d.c);
-    BARK_LAUNCH(tdt_proj_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, (const int*)d.state, (const float*)d.h,
+    BARK_LAUNCH(tdt_lstm0_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, 0, (const int*)d.state, next,
+                (const float4*)part, d.tokens, d.h, d.c);
+    BARK_LAUNCH(tdt_lstm1_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, (const int*)next, d.h, d.c);
+    BARK_LAUNCH(tdt_proj_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, d.state, (const int*)next, (const float*)d.h,
                 d.dec);
   }
   BARK_HIP_CHECK(hipGetLastError());

@@ -17,6 +17,9 @@ Also reported:
   gemm_lowbit  - the isolated 4-bit linear of configs[1] (bf16 activations,
                  bf16 out) at T in {188, 2207}, rotating >256 MB of distinct
                  codes/activations so the MALL cannot serve them;
+  mel_frontend - the GPU log-mel front end on the workload's 176.56 s of audio;
+  tdt_decoder  - the greedy TDT decoder over a T = 2207 synthetic pooler in
+                 HBM with synthetic decoder weights (ms per decode, tokens);
   cpu_baseline - the CPU oracle (C restatement of the reference CPU backend)
                  on this host's cores: by default the complete workload
                  (--cpu-blocks 24); fewer blocks time a sample and scale the
@@ -177,6 +180,47 @@ def cpu_mel(pkg) -> float:
     return (time.perf_counter() - t0) * 1e3
 
 
+TDT_T = 2207  # encoder frames of the workload
+
+
+def bench_tdt(pkg, synth, torch, reps: int = 5):
+    """Greedy TDT decoder (bark_hip_tdt_decode_device) over a synthetic pooler
+    of the workload's T frames resident in HBM, synthetic decoder weights
+    (synth.SynthTdt): wall time per decode (the call returns with the tokens in
+    host memory) and the GPU time of its launches."""
+    enc = pkg.HipEncoder.load_with(synth.SynthCheckpoint(seed=1, n_layers=1), 0, 1, front_end=False,
+                                   decoder=synth.SynthTdt(seed=0))
+    pooler = synth.pooler(TDT_T, 9)
+    d_p = torch.from_numpy(pooler).cuda()
+    sp = torch.cuda.current_stream().cuda_stream
+    torch.cuda.synchronize()
+    for _ in range(2):
+        toks = enc.tdt_decode_device(d_p.data_ptr(), TDT_T, sp)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        toks = enc.tdt_decode_device(d_p.data_ptr(), TDT_T, sp)
+        times.append(time.perf_counter() - t0)
+    enc.profile(True)
+    enc.tdt_decode_device(d_p.data_ptr(), TDT_T, sp)
+    rep = enc.profile_report()["tdt_decode"]
+    enc.profile(False)
+    enc.close()
+    ms = sorted(times)[len(times) // 2] * 1e3
+    return {"T": TDT_T, "audio_s": AUDIO_S, "tokens": int(len(toks)), "ms": ms, "gpu_ms": rep["ms"],
+            "us_per_frame": ms * 1e3 / TDT_T, "audio_s_per_s": AUDIO_S / (ms / 1e3)}
+
+
+def cpu_tdt(synth) -> dict:
+    """The numpy oracle's decode of the same pooler (ms) and its step count."""
+    from oracle import tdt as otdt
+
+    d = otdt.Decoder(synth.SynthTdt(seed=0))
+    t0 = time.perf_counter()
+    toks, margins = d.decode(synth.pooler(TDT_T, 9), with_margins=True)
+    return {"cpu_ms": (time.perf_counter() - t0) * 1e3, "steps": int(len(margins)), "cpu_tokens": int(len(toks))}
+
+
 def cpu_baseline(synth, blocks: int):
     """Oracle timing on this host's cores. blocks == 24 runs the complete
     workload (front end over the 17656-frame mel, 24 blocks, projector);
@@ -305,8 +349,15 @@ def main() -> int:
     log(f"[bench] log-mel front end: {mel['gpu_ms']:.3f} ms for {mel['audio_s']:.2f} s of audio "
         f"({mel['audio_s_per_s']:.0f} audio s/s)")
 
+    tdt = bench_tdt(pkg, synth, torch)
+    log(f"[bench] TDT decode: {tdt['ms']:.2f} ms for T={tdt['T']} ({tdt['tokens']} tokens, "
+        f"{tdt['us_per_frame']:.1f} us/frame, {tdt['audio_s_per_s']:.0f} audio s/s)")
+
     cpu = None
     if not args.no_cpu:
+        tdt.update(cpu_tdt(synth))
+        tdt["cpu_kind"] = "port (numpy oracle, oracle/tdt.py, float64)"
+        log(f"[bench] TDT decode on the CPU oracle: {tdt['cpu_ms']:.1f} ms ({tdt['steps']} steps)")
         mel["cpu_ms"] = cpu_mel(pkg)
         mel["cpu_kind"] = "port (numpy oracle, oracle/mel.py)"
         log(f"[bench] log-mel on the CPU oracle: {mel['cpu_ms']:.1f} ms")
@@ -336,6 +387,7 @@ def main() -> int:
         "breakdown": breakdown,
         "gemm_lowbit": gemm,
         "mel_frontend": mel,
+        "tdt_decoder": tdt,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
