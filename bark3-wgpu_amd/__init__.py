@@ -160,6 +160,10 @@ _SIGS = {
         _c.c_int,
         [_c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_size_t, _c.POINTER(_c.c_int32), _c.c_void_p],
     ),
+    "bark_hip_transcribe_wave_batch": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_void_p, _c.c_size_t, _c.c_void_p],
+    ),
     "bark_hip_profile": (_c.c_int, [_c.c_void_p, _c.c_int]),
     "bark_hip_profile_only": (_c.c_int, [_c.c_void_p, _c.c_char_p]),
     "bark_hip_profile_report": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_size_t]),
@@ -432,6 +436,25 @@ class HipEncoder:
             )
         )
         return out[: n.value].copy()
+
+    def transcribe_wave_batch(self, waves: Sequence[np.ndarray]) -> list[np.ndarray]:
+        """Log-mel, one batched encode and the greedy TDT decode of every 16 kHz
+        wave, poolers kept on the device; one (n, 3) u32 token array per wave."""
+        ws = [np.ascontiguousarray(w, dtype=np.float32) for w in waves]
+        n = np.asarray([w.size for w in ws], np.int64)
+        flat = np.ascontiguousarray(np.concatenate(ws))
+        ts = [conv_len(conv_len(conv_len(1 + int(k) // 160))) for k in n]
+        cap = sum(t * 14 + 64 for t in ts)
+        out = np.zeros((cap, 3), np.uint32)
+        counts = np.zeros(len(ws), np.int32)
+        t_out = np.zeros(len(ws), np.int32)
+        _check(lib().bark_hip_transcribe_wave_batch(self._h, _ptr(flat), _ptr(n), len(ws), _ptr(t_out), _ptr(out),
+                                                    cap, _ptr(counts)))
+        res, row = [], 0
+        for c in counts:
+            res.append(out[row : row + int(c)].copy())
+            row += int(c)
+        return res
 
     def profile(self, enable: bool = True) -> None:
         """Per-operator HIP-event timing of the forward (BARK3_ENC_PROFILE)."""

@@ -940,9 +940,12 @@ struct BarkHip {
 
   // Shared body of the mel-input entry points; pooler rows of sequence i are
   // written to out + (sum of earlier t) * 640 with `kind` host or device.
+  // out == nullptr leaves the poolers in the workspace (sequence i at row
+  // rows_out[i].first, rows_out[i].second rows) for a decode that follows.
   void encode_mel_batch(const float* mel_in, bool mel_on_device, const int32_t* frames,
                         const int32_t* valid, int batch, int32_t* t_out, float* out,
-                        bool out_on_device, size_t cap, hipStream_t st) {
+                        bool out_on_device, size_t cap, hipStream_t st,
+                        std::vector<std::pair<int, int>>* rows_out = nullptr) {
     BARK_REQUIRE(finalized, "encode before finalize");
     BARK_REQUIRE(batch >= 1 && frames, "batch must be >= 1");
     Plan pl = make_plan(frames, valid, nullptr, batch);
@@ -951,7 +954,7 @@ struct BarkHip {
       need_out += (size_t)s.t * PROJ;
       total_frames += (size_t)s.frames;
     }
-    BARK_REQUIRE(cap >= need_out, "pooler capacity too small");
+    BARK_REQUIRE(!out || cap >= need_out, "pooler capacity too small");
     ensure_workspace(pl);
     ensure_front_end(pl);
     const float* dmel = mel_in;
@@ -970,9 +973,12 @@ struct BarkHip {
     }
     encoder_blocks(pl, -1, st);
     size_t orow = 0;
+    if (rows_out) rows_out->clear();
     for (size_t i = 0; i < pl.seqs.size(); ++i) {
       const auto& s = pl.seqs[i];
       if (t_out) t_out[i] = s.t;
+      if (rows_out) rows_out->push_back({s.start, s.t});
+      if (!out) continue;
       const float* src = pooler.as<float>() + (size_t)s.start * PROJ;
       BARK_HIP_CHECK(hipMemcpyAsync(out + orow * PROJ, src, (size_t)s.t * PROJ * 4,
                                     out_on_device ? hipMemcpyDeviceToDevice
@@ -980,7 +986,7 @@ struct BarkHip {
                                     st));
       orow += s.t;
     }
-    if (!out_on_device) BARK_HIP_CHECK(hipStreamSynchronize(st));
+    if (out && !out_on_device) BARK_HIP_CHECK(hipStreamSynchronize(st));
   }
 
   // log-mel of each wave (packed frames), then one batched encode
@@ -1007,6 +1013,51 @@ struct BarkHip {
       foff += (size_t)frames[i];
     }
     encode_mel_batch(mel.as<float>(), true, frames.data(), valid.data(), batch, t_out, out, false, cap, st);
+  }
+
+  // Transcription of a batch of waves up to the tokens (AsrInference's
+  // mel -> encoder -> decoder, src/transcription.rs:56-224, chunk by chunk as
+  // src/inference.rs:298-386): log-mel of every wave, one batched encode, and
+  // a greedy TDT decode of each wave's pooler where the encoder left it; only
+  // the tokens leave the device. Wave i's n_tokens[i] {id, frame, dur} triples
+  // follow those of the waves before it.
+  void transcribe_wave_batch(const float* waves, const int64_t* n_samples, int batch, int32_t* t_out,
+                             uint32_t* tokens, size_t cap, int32_t* n_tokens) {
+    BARK_REQUIRE(has_tdt, "no TDT decoder tensors were set before finalize");
+    BARK_REQUIRE(batch >= 1 && waves && n_samples && n_tokens, "batch must be >= 1");
+    std::vector<int32_t> frames(batch), valid(batch);
+    size_t total_samples = 0, total_frames = 0;
+    for (int i = 0; i < batch; ++i) {
+      BARK_REQUIRE(n_samples[i] > 0, "empty wave");
+      total_samples += (size_t)n_samples[i];
+      frames[i] = mel_frames(n_samples[i]);
+      total_frames += (size_t)frames[i];
+    }
+    hipStream_t st = stream;
+    ensure(mel_wave, total_samples * 4);
+    ensure(mel, total_frames * MEL * 4);
+    BARK_HIP_CHECK(hipMemcpyAsync(mel_wave.p, waves, total_samples * 4, hipMemcpyHostToDevice, st));
+    size_t soff = 0, foff = 0;
+    for (int i = 0; i < batch; ++i) {
+      run_mel(mel_wave.as<float>() + soff, (long)n_samples[i], mel.as<float>() + foff * MEL, (size_t)frames[i] * MEL,
+              &frames[i], &valid[i], st);
+      soff += (size_t)n_samples[i];
+      foff += (size_t)frames[i];
+    }
+    std::vector<std::pair<int, int>> rows;
+    encode_mel_batch(mel.as<float>(), true, frames.data(), valid.data(), batch, t_out, nullptr, true, 0, st, &rows);
+    size_t off = 0;
+    for (int i = 0; i < batch; ++i) {
+      const int n = tdt_decode(pooler.as<float>() + (size_t)rows[i].first * PROJ, rows[i].second, st);
+      n_tokens[i] = n;
+      BARK_REQUIRE(off + (size_t)n <= cap, "token buffer too small");
+      if (n > 0) {
+        BARK_REQUIRE(tokens, "null token buffer");
+        BARK_HIP_CHECK(hipMemcpyAsync(tokens + 3 * off, tdt_tokens.p, (size_t)n * 12, hipMemcpyDeviceToHost, st));
+        BARK_HIP_CHECK(hipStreamSynchronize(st));
+      }
+      off += (size_t)n;
+    }
   }
 
   void encode_sub(const float* sub_rows, int t, int dump_layer, float* out_pooler,
@@ -1304,6 +1355,16 @@ int bark_hip_tdt_decode_device(BarkHip* h, const float* d_pooler, int32_t t_len,
     BARK_HIP_CHECK(hipSetDevice(h->device));
     hipStream_t st = stream ? static_cast<hipStream_t>(stream) : h->stream;
     h->tdt_decode_copy(d_pooler, t_len, tokens, cap, n_tokens, st);
+  });
+}
+
+int bark_hip_transcribe_wave_batch(BarkHip* h, const float* waves, const int64_t* n_samples, int32_t batch,
+                                   int32_t* t_out, uint32_t* tokens, size_t cap, int32_t* n_tokens) {
+  return guarded([&] {
+    BARK_REQUIRE(h && waves && n_samples && n_tokens, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    h->transcribe_wave_batch(waves, n_samples, batch, t_out, tokens, cap, n_tokens);
   });
 }
 

@@ -20,6 +20,8 @@ Also reported:
   mel_frontend - the GPU log-mel front end on the workload's 176.56 s of audio;
   tdt_decoder  - the greedy TDT decoder over a T = 2207 synthetic pooler in
                  HBM with synthetic decoder weights (ms per decode, tokens);
+  pipeline_wave_to_tokens - the workload's wave from host memory through
+                 log-mel, encoder and TDT decoder to tokens in one call;
   cpu_baseline - the CPU oracle (C restatement of the reference CPU backend)
                  on this host's cores: by default the complete workload
                  (--cpu-blocks 24); fewer blocks time a sample and scale the
@@ -65,7 +67,9 @@ def log(msg: str) -> None:
 def bench_encoder(pkg, synth, torch, steps: int, warmup: int):
     src = synth.SynthCheckpoint(seed=0, n_layers=24, style="baseline", lowbit=True)
     t0 = time.time()
-    enc = pkg.HipEncoder.load_with(src, device=0, n_layers=24)
+    # the decoder's weights ride along for the wave -> tokens pipeline measured
+    # after the encoder (they do not touch the encoder step)
+    enc = pkg.HipEncoder.load_with(src, device=0, n_layers=24, decoder=synth.SynthTdt(seed=0))
     log(f"[bench] weights loaded in {time.time() - t0:.1f}s")
     mel = torch.from_numpy(synth.mel(FRAMES, seed=0)).cuda()
     T = pkg.conv_len(pkg.conv_len(pkg.conv_len(FRAMES)))
@@ -99,8 +103,29 @@ def bench_encoder(pkg, synth, torch, steps: int, warmup: int):
     timed = enc.profile_report()[dom]
     enc.profile(False)
     log(f"[bench] encoder step {dt * 1e3:.3f} ms over {steps} steps (T={T})")
+    pipe = bench_pipeline(enc)
     enc.close()
-    return dt, T, prof, dom, timed
+    return dt, T, prof, dom, timed, pipe
+
+
+def bench_pipeline(enc, reps: int = 3):
+    """bark_hip_transcribe_wave_batch on the workload's 176.56 s wave from host
+    memory: upload, log-mel, the 24-block encoder and the greedy TDT decode of
+    the pooler in device memory, tokens back to the host. The synthetic
+    encoder's outputs are small, so the decoder's biases decide its steps."""
+    enc.set_mel_filters()
+    wave = mel_wave()
+    toks = enc.transcribe_wave_batch([wave])[0]
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        toks = enc.transcribe_wave_batch([wave])[0]
+        times.append(time.perf_counter() - t0)
+    ms = sorted(times)[len(times) // 2] * 1e3
+    audio_s = wave.size / 16000.0
+    log(f"[bench] wave -> tokens pipeline: {ms:.2f} ms for {audio_s:.2f} s of audio ({len(toks)} tokens)")
+    return {"audio_s": audio_s, "ms": ms, "audio_s_per_s": audio_s / (ms / 1e3), "tokens": int(len(toks)),
+            "includes": "host->device wave upload (11.3 MB), log-mel, 24-block encoder, TDT decode, tokens to host"}
 
 
 def bench_gemm(pkg, torch, T: int, K: int, N: int, reps: int = 192):
@@ -307,7 +332,7 @@ def main() -> int:
         traffic_workload(pkg, synth, torch)
         return 0
 
-    dt, T, prof, dom, d = bench_encoder(pkg, synth, torch, args.steps, args.warmup)
+    dt, T, prof, dom, d, pipe = bench_encoder(pkg, synth, torch, args.steps, args.warmup)
     # roofline of the dominant kernel from its launches inside the timed region
     # (every profiled label is one kernel, so this is rocprof's average duration)
     avg_s = d["ms"] / d["count"] / 1e3
@@ -384,6 +409,7 @@ def main() -> int:
         "gemm_lowbit": gemm,
         "mel_frontend": mel,
         "tdt_decoder": tdt,
+        "pipeline_wave_to_tokens": pipe,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

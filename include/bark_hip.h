@@ -131,6 +131,19 @@ int bark_hip_tdt_decode(BarkHip *h, const float *pooler, int32_t t_len, uint32_t
 int bark_hip_tdt_decode_device(BarkHip *h, const float *d_pooler, int32_t t_len, uint32_t *tokens,
                                size_t cap, int32_t *n_tokens, void *stream);
 
+/* Transcription up to the tokens (AsrInference::transcribe's mel -> encoder
+ * -> decoder, src/transcription.rs:56-224, over the VAD chunks of
+ * src/inference.rs:298-386): log-mel of each 16 kHz wave, one batched encode,
+ * and the greedy TDT decode of each wave's pooler in device memory (the pooler
+ * never leaves the device, as with the reference's pooler_buf,
+ * src/transcription.rs:200-209). t_out[i] (may be NULL) receives wave i's T;
+ * n_tokens[i] its token count; tokens receives every wave's {id, frame, dur}
+ * triples back to back in wave order (cap counts triples; sum of
+ * T_i * 14 + 64 always suffices). Needs the decoder's tensors. */
+int bark_hip_transcribe_wave_batch(BarkHip *h, const float *waves, const int64_t *n_samples,
+                                   int32_t batch, int32_t *t_out, uint32_t *tokens, size_t cap,
+                                   int32_t *n_tokens);
+
 /* Per-operator GPU timing, the counterpart of BARK3_ENC_PROFILE
  * (src/encoder/prof.rs:1-127, src/encoder.rs:823-827): while enabled, every
  * launch of the forward is bracketed by HIP events on its stream. Enabling or

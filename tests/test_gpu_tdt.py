@@ -133,3 +133,22 @@ def test_tdt_repeat_after_other_lengths(base, synth):
     base.tdt_decode(synth.pooler(1000, 2))
     base.tdt_decode(synth.pooler(1, 4))
     np.testing.assert_array_equal(base.tdt_decode(p), first)
+
+
+def test_transcribe_wave_batch(pkg, synth):
+    """waves -> tokens in one call (poolers stay on the device) equals the
+    batched wave encode followed by a decode of each returned pooler"""
+    print("case tdt transcribe waves", flush=True)
+    enc = make(pkg, synth, seed=0, blank_bias=-1.0)
+    try:
+        enc.set_mel_filters()
+        rng = np.random.default_rng(7)
+        waves = [(0.1 * rng.standard_normal(n)).astype(np.float32) for n in (48000, 16077, 5000)]
+        got = enc.transcribe_wave_batch(waves)
+        poolers = enc.encode_wave_batch(waves)
+        assert len(got) == len(poolers) == 3
+        for g, p in zip(got, poolers):
+            np.testing.assert_array_equal(g, enc.tdt_decode(p))
+        assert sum(len(g) for g in got) > 0
+    finally:
+        enc.close()
