@@ -122,6 +122,7 @@ _SIGS = {
         [_c.c_void_p, _c.c_char_p, _c.c_void_p, _c.c_void_p, _c.c_uint32, _c.c_int64, _c.c_int64],
     ),
     "bark_hip_set_lut4": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64]),
+    "bark_hip_load_safetensors": (_c.c_int, [_c.c_void_p, _c.c_char_p]),
     "bark_hip_finalize": (_c.c_int, [_c.c_void_p]),
     "bark_hip_encode_sub": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_int32, _c.c_void_p, _c.c_void_p]),
     "bark_hip_encode_mel": (
@@ -273,6 +274,11 @@ class HipEncoder:
                 a32 = np.ascontiguousarray(arr, dtype=np.float32)
                 shape = (ctypes.c_int64 * max(a32.ndim, 1))(*(a32.shape or (1,)))
                 _check(L.bark_hip_set_f32(self._h, n, _ptr(a32), shape, max(a32.ndim, 1)))
+
+    def load_safetensors(self, path) -> None:
+        """Stage every tensor this handle reads from a safetensors checkpoint
+        (a file, or a directory with model.safetensors or an index and shards)."""
+        _check(lib().bark_hip_load_safetensors(self._h, str(path).encode()))
 
     def finalize(self) -> None:
         _check(lib().bark_hip_finalize(self._h))

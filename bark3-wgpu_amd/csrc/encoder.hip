@@ -1227,6 +1227,66 @@ int bark_hip_set_lut4(BarkHip* h, const char* name, const uint8_t* codes, const 
   });
 }
 
+int bark_hip_load_safetensors(BarkHip* h, const char* path) {
+  return guarded([&] {
+    BARK_REQUIRE(h && path, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_REQUIRE(!h->finalized, "tensors cannot be set after finalize");
+    // the tensors this handle reads: front end, encoder blocks below n_layers,
+    // projector, TDT decoder and joint
+    auto wanted = [&](const std::string& n) {
+      const std::string blocks = "encoder.layers.";
+      if (n.compare(0, blocks.size(), blocks) == 0) {
+        const size_t dot = n.find('.', blocks.size());
+        if (dot == std::string::npos) return false;
+        const std::string l = n.substr(blocks.size(), dot - blocks.size());
+        if (l.empty() || l.size() > 3 || l.find_first_not_of("0123456789") != std::string::npos) return false;
+        return std::stoi(l) < h->n_layers;
+      }
+      for (const char* pre : {"encoder.subsampling.", "encoder_projector.", "decoder.", "joint."})
+        if (n.compare(0, std::strlen(pre), pre) == 0) return true;
+      return false;
+    };
+    for (const std::string& file : safetensors_files(path)) {
+      for (const StTensor& t : safetensors_header(file)) {
+        if (!wanted(t.name)) continue;
+        int64_t n = 1;
+        for (int64_t d : t.shape) n *= d;
+        const uint64_t bytes = t.end - t.begin;
+        HostTensor v;
+        v.shape = t.shape;
+        if (t.dtype == "F32") {
+          BARK_REQUIRE(bytes == (uint64_t)n * 4, t.name + ": size does not match its shape");
+          v.kind = HostTensor::F32;
+          v.f32.resize(n);
+          safetensors_read(file, t, v.f32.data());
+        } else if (t.dtype == "F16") {
+          BARK_REQUIRE(bytes == (uint64_t)n * 2, t.name + ": size does not match its shape");
+          v.kind = HostTensor::F16;
+          v.f16.resize(n);
+          safetensors_read(file, t, v.f16.data());
+          v.rows = t.shape.empty() ? 1 : t.shape[0];
+          v.cols = v.rows ? n / v.rows : 0;
+        } else if (t.dtype == "BF16") {  // widened exactly (RawTensor::to_f32, src/raw.rs:23-48)
+          BARK_REQUIRE(bytes == (uint64_t)n * 2, t.name + ": size does not match its shape");
+          std::vector<uint16_t> raw(n);
+          safetensors_read(file, t, raw.data());
+          v.kind = HostTensor::F32;
+          v.f32.resize(n);
+          for (int64_t k = 0; k < n; ++k) {
+            const uint32_t u = (uint32_t)raw[k] << 16;
+            std::memcpy(&v.f32[k], &u, 4);
+          }
+        } else {
+          continue;  // integer entries (BatchNorm's num_batches_tracked) are never read
+        }
+        BARK_REQUIRE(n > 0, t.name + ": empty tensor");
+        stage(h, t.name.c_str()) = std::move(v);
+      }
+    }
+  });
+}
+
 int bark_hip_finalize(BarkHip* h) {
   return guarded([&] {
     BARK_REQUIRE(h, "null handle");

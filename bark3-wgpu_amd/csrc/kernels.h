@@ -3,6 +3,8 @@
 // shapes the kernels assume, and throw bark::Error on a mismatch.
 #pragma once
 
+#include <vector>
+
 #include "common.h"
 
 namespace bark {
@@ -191,5 +193,19 @@ int tdt_max_steps(int t_len);
 void tdt_begin(const TdtDev& d, int t_len, int cap, hipStream_t st);
 // queue `steps` decode steps (steps after the end return at once)
 void tdt_steps(const TdtDev& d, const float* pooler, int steps, hipStream_t st);
+
+// ---------------------------------------------------------- safetensors --
+// One tensor entry of a safetensors header (ingest.hip); begin / end are
+// absolute byte offsets in its file.
+struct StTensor {
+  std::string name, dtype;
+  std::vector<int64_t> shape;
+  uint64_t begin = 0, end = 0;
+};
+// the files of a checkpoint: a .safetensors file, or a directory holding
+// model.safetensors or model.safetensors.index.json and its shards
+std::vector<std::string> safetensors_files(const std::string& path);
+std::vector<StTensor> safetensors_header(const std::string& file);
+void safetensors_read(const std::string& file, const StTensor& t, void* dst);
 
 }  // namespace bark

@@ -71,6 +71,15 @@ int bark_hip_set_lowbit(BarkHip *h, const char *name, const uint32_t *codes,
  * even column), lut16 rows x 16 f16. Byte-identical code layout to the above. */
 int bark_hip_set_lut4(BarkHip *h, const char *name, const uint8_t *codes,
                       const uint16_t *lut16, int64_t rows, int64_t cols);
+/* TensorReader::open_model + read (src/weights_io.rs:46-127) feeding the
+ * calls above: stages every tensor this handle reads (front end, encoder
+ * blocks below n_layers, projector, TDT decoder and joint) from a safetensors
+ * checkpoint. `path` is a .safetensors file or a model directory holding
+ * model.safetensors, or model.safetensors.index.json and its shards. F32 and
+ * F16 entries are taken as stored, BF16 widened exactly to f32 (linears are
+ * then rounded to f16 as with bark_hip_set_f32); integer entries are skipped.
+ * Tensors are read one at a time. Call before bark_hip_finalize. */
+int bark_hip_load_safetensors(BarkHip *h, const char *path);
 /* Fuses q|k|v (load_qkv, src/encoder.rs:342-402), folds BatchNorm
  * (src/encoder.rs:546-557), interleaves pw1 rows for the GLU epilogue and
  * uploads everything. Returns BARK_HIP_EINVAL naming a missing tensor. */
