@@ -543,7 +543,7 @@ struct BarkHip {
     ensure(tdt_h, 4 * DH * 4);
     ensure(tdt_c, 2 * DH * 4);
     ensure(tdt_dec, DH * 4);
-    ensure(tdt_part, TDT_PARTIALS * 16);
+    ensure(tdt_part, 2 * TDT_PARTIALS * 16);
     BARK_HIP_CHECK(hipHostMalloc((void**)&tdt_host, (size_t)tdt_state_words() * 4, hipHostMallocDefault));
     tdt.state = tdt_state.as<int>();
     tdt.h = tdt_h.as<float>();
@@ -554,9 +554,9 @@ struct BarkHip {
 
   // Greedy TDT decoding of a device pooler (t_len x 640 f32) on `st`
   // (TdtDecoder::decode, src/tdt.rs:318-414; GpuTdtDecoder::decode_async,
-  // src/tdt_gpu.rs:206-300). Steps are queued in chunks; after each chunk only
-  // the state words come back, and decoding ends when the device sets `done`.
-  // Returns the number of tokens; their {id, frame, dur} words stay in
+  // src/tdt_gpu.rs:206-300). Launches are queued in chunks; after each chunk
+  // only the control state comes back, and decoding ends when the device sets
+  // `done`. Returns the number of tokens; their {id, frame, dur} words stay in
   // tdt_tokens.
   int tdt_decode(const float* d_pooler, int t_len, hipStream_t st) {
     BARK_REQUIRE(finalized, "decode before finalize");
@@ -564,6 +564,7 @@ struct BarkHip {
     BARK_REQUIRE(t_len >= 0 && t_len <= (1 << 24), "t_len out of range");
     if (t_len == 0) return 0;  // src/tdt_gpu.rs:211-216
     const int max_steps = tdt_max_steps(t_len);
+    const long max_launches = tdt_max_launches(t_len);
     ensure(tdt_tokens, (size_t)max_steps * 12);
     TdtDev d = tdt;
     d.tokens = tdt_tokens.as<uint32_t>();
@@ -571,18 +572,19 @@ struct BarkHip {
     const double step_bytes = 2.0 * 640 * (8198 + 4 * 2560 + 640);
     const size_t words = (size_t)tdt_state_words() * 4;
     tdt_begin(d, t_len, max_steps, st);
-    int steps = 0, chunk = std::max(16, t_len / 2);
+    long launches = 0;
+    long chunk = std::max(16, t_len / 2);
     while (true) {
-      const int n = std::min(chunk, max_steps - steps);
-      prof.run("tdt_decode", 0, step_bytes * n, st, [&] { tdt_steps(d, d_pooler, n, st); });
-      steps += n;
-      BARK_HIP_CHECK(hipMemcpyAsync(tdt_host, d.state, words, hipMemcpyDeviceToHost, st));
+      const int n = (int)std::min(chunk, max_launches - launches);
+      prof.run("tdt_decode", 0, step_bytes * n / 4, st, [&] { tdt_launches(d, d_pooler, n, launches, st); });
+      BARK_HIP_CHECK(
+          hipMemcpyAsync(tdt_host, tdt_current(d, launches), words, hipMemcpyDeviceToHost, st));
       BARK_HIP_CHECK(hipStreamSynchronize(st));
-      if (tdt_host[tdt_done_word()] || steps >= max_steps) break;
-      // the rest at the rate seen so far (steps per frame), plus a margin
+      if (tdt_host[tdt_done_word()] || launches >= max_launches) break;
+      // the rest at the rate seen so far (launches per frame), plus a margin
       const int frame = tdt_host[tdt_frame_word()];
-      const double rate = (double)steps / std::max(frame, 1);
-      chunk = std::max(16, (int)(rate * (t_len - frame)) + 8);
+      const double rate = (double)launches / std::max(frame, 1);
+      chunk = std::max(16L, (long)(rate * (t_len - frame)) + 8);
     }
     BARK_REQUIRE(tdt_host[tdt_done_word()], "TDT decoding did not finish within the step guard");
     return tdt_host[tdt_count_word()];

@@ -173,7 +173,7 @@ void mel_features(const float* wave, long n_samples, const MelTables& tb, void* 
 // and biases f32; LSTM (2 layers x 2560 x 640, ih and hh), projection
 // (640 x 640) and joint head (8198 x 640) f16; state words (the current
 // control state, then the next one); h (2 layers x 2
-// buffers x 640), c (2 x 640), dec (640), joint partials (256 float4),
+// buffers x 640), c (2 x 640), dec (640), joint partials (2 x 256 float4),
 // tokens (cap x {id, frame, dur}).
 struct TdtDev {
   const float* embed = nullptr;
@@ -183,16 +183,20 @@ struct TdtDev {
   float *h = nullptr, *c = nullptr, *dec = nullptr, *partials = nullptr;
   uint32_t* tokens = nullptr;
 };
-constexpr int TDT_PARTIALS = 256;  // workgroups of a phase, one joint partial each
+constexpr int TDT_PARTIALS = 256;  // joint partials per set (the largest grid); two sets
 int tdt_state_words();  // words of one control state (the buffer holds two)
 int tdt_frame_word();  // index of the frame pointer among the state words
 int tdt_done_word();   // index of the `done` flag
 int tdt_count_word();  // index of the emitted-token count
 int tdt_max_steps(int t_len);
-// reset the state for a pooler of t_len frames and run the start LSTM step
+long tdt_max_launches(int t_len);  // launches after which `done` is certain
+// reset the control state for a pooler of t_len frames (the start step pending)
 void tdt_begin(const TdtDev& d, int t_len, int cap, hipStream_t st);
-// queue `steps` decode steps (steps after the end return at once)
-void tdt_steps(const TdtDev& d, const float* pooler, int steps, hipStream_t st);
+// queue n launches, each running the phase the control state names; `launches`
+// counts them from tdt_begin (it selects the state buffer)
+void tdt_launches(const TdtDev& d, const float* pooler, int n, long& launches, hipStream_t st);
+// the state buffer that holds the control state after `launches` launches
+const int* tdt_current(const TdtDev& d, long launches);
 
 // ---------------------------------------------------------- safetensors --
 // One tensor entry of a safetensors header (ingest.hip); begin / end are

@@ -3,42 +3,45 @@
 // emitted tokens kept in device memory, as GpuTdtDecoder does
 // (src/tdt_gpu.rs:1-7, 206-300).
 //
-// A decode step is four launches on one stream; each reads only what the
-// launches before it wrote, so kernel boundaries are the only synchronisation,
-// and the control state (frame, step count, parity of the h buffers, whether
-// the LSTM runs) lives in device memory:
+// The decode is a chain of launches of one kernel on one stream; each launch
+// runs the phase its control state (in device memory) names and leaves the
+// next control state, so kernel boundaries are the only synchronisation:
 //   joint  x = relu(pooler[frame] + dec); scores of the 8198 head rows (8193
 //          tokens + 5 durations, f16 weights, f32 sums, src/tdt.rs:217-288)
 //          over G workgroups, each leaving its best token and best duration;
-//   lstm0  every workgroup reduces the partials to the step's decision (the
-//          same everywhere) and workgroup 0 applies it to the next control
-//          state: blank: frame += max(dur, 1); token: record {id, frame, dur},
-//          frame += dur (src/tdt.rs:386-412); `done` once the loop would exit
-//          (frame >= T or the step guard T * 14 + 64). For a token that does
-//          not end the decode, LSTM layer 0 on its embedding: one wave per
-//          channel holds its i, f, g, o gate rows of w_ih and w_hh (8 row
-//          dots, 8 lanes each), gate = b_ih + b_hh + w_ih.x + w_hh.h_old,
-//          c = f c + i g, h = o tanh(c) (src/tdt.rs:179-214);
+//   decide every workgroup reduces the partials to the step's decision (the
+//          same everywhere): blank: frame += max(dur, 1) (src/tdt.rs:386-412),
+//          and the next step's joint runs in the same launch (dec is
+//          unchanged); token: record {id, frame, dur}, frame += dur, and LSTM
+//          layer 0 on its embedding in the same launch: one wave per channel
+//          holds its i, f, g, o gate rows of w_ih and w_hh (8 row dots, 8 lanes
+//          each), gate = b_ih + b_hh + w_ih.x + w_hh.h_old, c = f c + i g,
+//          h = o tanh(c) (src/tdt.rs:179-214); `done` once the loop would exit
+//          (frame >= T or the step guard T * 14 + 64);
 //   lstm1  layer 1 on the new h0;
-//   proj   dec = b + W h1 (src/tdt.rs:515-529); workgroup 0 makes the next
-//          control state the current one.
-// Launches after `done`, and lstm1 / proj after a blank, return at once. The
-// host queues steps in chunks and reads back only the state words. Row dots
-// read each 1280-byte f16 row with 8 lanes (ten 16-byte loads each, issued
-// before the input vector is staged in LDS or the decision is known, so the
-// loads overlap).
+//   proj   dec = b + W h1 (src/tdt.rs:515-529).
+// A blank step costs one launch, a token step four (decide, lstm1, proj,
+// joint). The host queues launches in chunks and reads back only the control
+// state. Row dots read each 1280-byte f16 row with 8 lanes (ten 16-byte loads
+// each, issued before the input vector is staged in LDS or the decision is
+// known, so the loads overlap).
 //
-// Measured alternatives: deciding in the joint's last workgroup (an arrival
-// counter) and a single cooperative launch with grid barriers between the
-// phases were both slower than these launch boundaries (arrivals of 256
-// workgroups on one counter serialise; a cross-XCD barrier costs more than a
-// dependent launch).
+// Measured alternatives (T = 2207, 1267 steps): one launch per phase with a
+// separate one-wave decision, 24.4 ms; the decision folded into the layer-0
+// launch (four launches every step), 19-21 ms; this phase chain, 16 ms. The
+// decision in the joint's last workgroup via an arrival counter (256 arrivals
+// on one counter serialise) and a single cooperative launch with grid
+// barriers between the phases (a cross-XCD barrier costs more than a dependent
+// launch) were both slower.
 //
 // The argmax order is total — higher score first, then the lower row — so the
 // result does not depend on how rows are spread over workgroups and lanes and
 // equals the reference's first-maximum scan. Dot products are f32 sums in a
 // different order than the reference's 8-lane AVX blocks, so scores agree to
 // rounding and greedy decisions agree unless two scores tie to within it.
+#include <cstdio>
+#include <cstdlib>
+
 #include "kernels.h"
 
 namespace bark {
@@ -51,7 +54,7 @@ constexpr int ROW_LOADS = DH / 8 / 8;  // 16-byte loads per lane per row (10)
 constexpr int NONE = 0x7fffffff;
 
 // state words (int32)
-enum { S_FRAME, S_DONE, S_NTOK, S_GUARD, S_TOKEN, S_EMIT, S_PAR, S_LSTM, S_TLEN, S_MAXSTEPS, S_CAP, S_WORDS };
+enum { S_PHASE, S_FRAME, S_DONE, S_NTOK, S_GUARD, S_PAR, S_LSTM, S_PQ, S_TLEN, S_MAXSTEPS, S_CAP, S_WORDS };
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
 __device__ inline float2 halves(uint32_t u) {
@@ -124,19 +127,24 @@ struct Weights {
 
 // ---------------------------------------------------------------- phases --
 
-// joint scores of rows wg, wg + G, ... ; the workgroup's best token and best
-// duration go to part[wg]
-__device__ void phase_joint(const Weights& W, const float* enc, const float* dec, float4* part, int G, int wg,
-                            Lds& sh) {
-  const int grp = threadIdx.x >> 3, sub = threadIdx.x & 7;
-  const int r = wg + G * grp;
-  Row row;
-  if (r < NROWS) row.load(W.head_w + (size_t)r * DH, sub);
+// the head row of this lane group in the joint: rows wg, wg + G, ...
+__device__ inline bool joint_row(const Weights& W, int G, int wg, Row& row) {
+  const int r = wg + G * (threadIdx.x >> 3);
+  if (r >= NROWS) return false;
+  row.load(W.head_w + (size_t)r * DH, threadIdx.x & 7);
+  return true;
+}
+
+// joint scores of rows wg, wg + G, ... (rows loaded by joint_row); the
+// workgroup's best token and best duration go to part[wg]
+__device__ void phase_joint(const Weights& W, const Row& row, bool has_row, const float* enc, const float* dec,
+                            float4* part, int G, int wg, Lds& sh) {
   for (int k = threadIdx.x; k < DH; k += THREADS) sh.xs[k] = fmaxf(enc[k] + dec[k], 0.0f);
   __syncthreads();
   Best b{-INFINITY, -INFINITY, NONE, NONE};
-  if (r < NROWS) {
-    const float sc = W.head_b[r] + row.dot(sh.xs, sub);
+  if (has_row) {
+    const int r = wg + G * (threadIdx.x >> 3);
+    const float sc = W.head_b[r] + row.dot(sh.xs, threadIdx.x & 7);
     if (r < VOCAB)
       b.ts = sc, b.ti = r;
     else
@@ -228,111 +236,125 @@ __device__ void phase_proj(const Weights& W, const float* h1, float* dec, int G,
   }
 }
 
-// --------------------------------------------------------- stepped driver --
+// ---------------------------------------------------------- the launches --
 
-__global__ void __launch_bounds__(THREADS) tdt_joint_kernel(Weights W, const float* pooler, const float* dec,
-                                                            const int* state, float4* part) {
-  if (state[S_DONE]) return;
-  __shared__ Lds sh;
-  phase_joint(W, pooler + (size_t)state[S_FRAME] * DH, dec, part, gridDim.x, blockIdx.x, sh);
-}
+// Every launch runs the phase the control state names and leaves the next
+// control state in `out` (written by workgroup 0; `in` stays as it was, so
+// every workgroup reads the same values). Every workgroup reduces the joint
+// partials itself, so the decision needs no launch of its own:
+//   START   LSTM layer 0 on the blank embedding from h = c = 0   -> L1
+//   L1      LSTM layer 1 on the new h0                           -> PROJ
+//   PROJ    dec = b + W h1                                       -> JOINT
+//   JOINT   joint partials at `frame` into set q                 -> DECIDE
+//   DECIDE  decision from set q (src/tdt.rs:386-412):
+//             done (frame >= T or the step guard)                -> DONE
+//             blank: frame += max(dur, 1), joint partials at the
+//             new frame into set q ^ 1                           -> DECIDE
+//             token: record {id, frame, dur}, frame += dur,
+//             LSTM layer 0 on its embedding                      -> L1
+//   DONE    nothing
+// A run of blanks costs one launch per step; a token step four.
+enum { PH_START, PH_L1, PH_PROJ, PH_JOINT, PH_DECIDE, PH_DONE };
 
-// Layer 0 of the LSTM, preceded by the step's decision: every workgroup
-// reduces the joint partials itself (the same result everywhere), and
-// workgroup 0 writes the updated control state to `next` (the words this
-// launch reads stay unchanged until the projection copies `next` back).
-// blank: frame += max(dur, 1); token: record {id, frame, dur}, frame += dur,
-// and the LSTM runs on its embedding unless decoding ends here. With `start`
-// set this is the start step on the blank embedding from h = c = 0.
-__global__ void __launch_bounds__(THREADS) tdt_lstm0_kernel(Weights W, int start, const int* state, int* next,
-                                                            const float4* part, uint32_t* tokens, float* h,
-                                                            float* c) {
-  if (!start && state[S_DONE]) return;
+__global__ void __launch_bounds__(THREADS) tdt_advance_kernel(Weights W, const float* pooler, const int* in,
+                                                              int* out, float4* part, uint32_t* tokens, float* h,
+                                                              float* c, float* dec) {
   __shared__ Lds sh;
   const int G = gridDim.x, wg = blockIdx.x;
+  const int phase = in[S_PHASE];
+  // the control state this launch leaves (workgroup 0 writes it at the end)
+  int frame = in[S_FRAME], ntok = in[S_NTOK], guard = in[S_GUARD], lstm = in[S_LSTM], par = in[S_PAR];
+  int q = in[S_PQ], next = phase, done = in[S_DONE];
   Row row;
-  const bool has_row = lstm_row(W, 0, G, wg, row);
-  int tok = BLANK, p = 0;
-  if (!start) {
-    phase_decide(part, TDT_PARTIALS, sh);
-    tok = sh.tok;
-    const int dur = sh.dur;
-    int frame = state[S_FRAME], ntok = state[S_NTOK], lstm = state[S_LSTM];
-    const int guard = state[S_GUARD] + 1;
-    const bool token = tok != BLANK;
-    if (token) {
-      if (wg == 0 && threadIdx.x == 0 && ntok < state[S_CAP]) {
-        tokens[3 * ntok] = (uint32_t)tok;
-        tokens[3 * ntok + 1] = (uint32_t)frame;
-        tokens[3 * ntok + 2] = (uint32_t)dur;
-      }
-      ++ntok;
-      frame += dur;
-    } else {
-      frame += max(dur, 1);
+  bool has_row;
+  switch (phase) {
+    case PH_START:  // h[0][1] = lstm0(embed[blank]; h = c = 0)
+      has_row = lstm_row(W, 0, G, wg, row);
+      phase_lstm(W, 0, row, has_row, W.embed + (size_t)BLANK * DH, nullptr, h + DH, c, G, wg, sh);
+      next = PH_L1;
+      break;
+    case PH_L1: {  // h[1][par ^ 1] = lstm1(h[0][par ^ 1]; h[1][par])
+      has_row = lstm_row(W, 1, G, wg, row);
+      const bool first = lstm == 1;
+      phase_lstm(W, 1, row, has_row, h + (size_t)(par ^ 1) * DH, first ? nullptr : h + (size_t)(2 + par) * DH,
+                 h + (size_t)(2 + (par ^ 1)) * DH, c + DH, G, wg, sh);
+      next = PH_PROJ;
+      break;
     }
-    const bool done = frame >= state[S_TLEN] || guard >= state[S_MAXSTEPS];
-    // the new decoder state is only needed if another step follows
-    const bool emit = token && !done;
-    p = lstm & 1;
-    if (wg == 0 && threadIdx.x < S_WORDS) {
-      int v = state[threadIdx.x];
-      switch (threadIdx.x) {
-        case S_FRAME: v = frame; break;
-        case S_DONE: v = done; break;
-        case S_NTOK: v = ntok; break;
-        case S_GUARD: v = guard; break;
-        case S_TOKEN: v = emit ? tok : v; break;
-        case S_EMIT: v = emit; break;
-        case S_PAR: v = emit ? p : v; break;
-        case S_LSTM: v = emit ? lstm + 1 : v; break;
-        default: break;
+    case PH_PROJ:
+      phase_proj(W, h + (size_t)(2 + (par ^ 1)) * DH, dec, G, wg, sh);
+      next = PH_JOINT;
+      break;
+    case PH_JOINT:
+      has_row = joint_row(W, G, wg, row);
+      phase_joint(W, row, has_row, pooler + (size_t)frame * DH, dec, part + q * TDT_PARTIALS, G, wg, sh);
+      next = PH_DECIDE;
+      break;
+    case PH_DECIDE: {
+      has_row = joint_row(W, G, wg, row);  // the next joint's rows, in case this step is a blank
+      phase_decide(part + q * TDT_PARTIALS, G, sh);
+      const int tok = sh.tok, dur = sh.dur;
+      ++guard;
+      if (tok == BLANK) {
+        frame += max(dur, 1);
+      } else {
+        if (wg == 0 && threadIdx.x == 0 && ntok < in[S_CAP]) {
+          tokens[3 * ntok] = (uint32_t)tok;
+          tokens[3 * ntok + 1] = (uint32_t)frame;
+          tokens[3 * ntok + 2] = (uint32_t)dur;
+        }
+        ++ntok;
+        frame += dur;
       }
-      next[threadIdx.x] = v;
+      done = frame >= in[S_TLEN] || guard >= in[S_MAXSTEPS];
+      if (done) {
+        next = PH_DONE;
+      } else if (tok == BLANK) {  // dec is unchanged: the next step's joint right away
+        q ^= 1;
+        phase_joint(W, row, has_row, pooler + (size_t)frame * DH, dec, part + q * TDT_PARTIALS, G, wg, sh);
+      } else {
+        par = lstm & 1;
+        ++lstm;
+        has_row = lstm_row(W, 0, G, wg, row);
+        phase_lstm(W, 0, row, has_row, W.embed + (size_t)tok * DH, h + (size_t)par * DH, h + (size_t)(par ^ 1) * DH,
+                   c, G, wg, sh);
+        next = PH_L1;
+      }
+      break;
     }
-    if (!emit) return;
+    default:
+      break;
   }
-  const bool first = start != 0;
-  phase_lstm(W, 0, row, has_row, W.embed + (size_t)tok * DH, first ? nullptr : h + (size_t)p * DH,
-             h + (size_t)(p ^ 1) * DH, c, G, wg, sh);
+  if (wg == 0 && threadIdx.x < S_WORDS) {
+    int v = in[threadIdx.x];
+    switch (threadIdx.x) {
+      case S_PHASE: v = next; break;
+      case S_FRAME: v = frame; break;
+      case S_DONE: v = done; break;
+      case S_NTOK: v = ntok; break;
+      case S_GUARD: v = guard; break;
+      case S_PAR: v = par; break;
+      case S_LSTM: v = lstm; break;
+      case S_PQ: v = q; break;
+      default: break;
+    }
+    out[threadIdx.x] = v;
+  }
 }
 
-// layer 1: h[1][S_PAR] holds the old state, h[1][S_PAR ^ 1] receives the new
-// one; the input is the new h0 = h[0][S_PAR ^ 1]
-__global__ void __launch_bounds__(THREADS) tdt_lstm1_kernel(Weights W, const int* next, float* h, float* c) {
-  if (!next[S_EMIT]) return;
-  __shared__ Lds sh;
-  Row row;
-  const bool has_row = lstm_row(W, 1, gridDim.x, blockIdx.x, row);
-  const int p = next[S_PAR];
-  const bool first = next[S_LSTM] == 1;  // the start step: h = c = 0
-  phase_lstm(W, 1, row, has_row, h + (size_t)(p ^ 1) * DH, first ? nullptr : h + (size_t)(2 + p) * DH,
-             h + (size_t)(2 + (p ^ 1)) * DH, c + DH, gridDim.x, blockIdx.x, sh);
-}
-
-// dec = b + W h1_new, then workgroup 0 makes `next` the current state
-__global__ void __launch_bounds__(THREADS) tdt_proj_kernel(Weights W, int* state, const int* next, const float* h,
-                                                           float* dec) {
-  __shared__ Lds sh;
-  if (next[S_EMIT]) phase_proj(W, h + (size_t)(2 + (next[S_PAR] ^ 1)) * DH, dec, gridDim.x, blockIdx.x, sh);
-  if (blockIdx.x == 0 && threadIdx.x < S_WORDS) state[threadIdx.x] = next[threadIdx.x];
-}
-
-// both state copies: frame 0, the start step pending (blank, parity 0)
 __global__ void tdt_init_kernel(int* state, int t_len, int max_steps, int cap) {
-  if (threadIdx.x < 2) {
-    int* s = state + threadIdx.x * S_WORDS;
-    s[S_FRAME] = 0;
-    s[S_DONE] = t_len <= 0;
-    s[S_NTOK] = 0;
-    s[S_GUARD] = 0;
-    s[S_TOKEN] = BLANK;
-    s[S_EMIT] = 1;
-    s[S_PAR] = 0;
-    s[S_LSTM] = 1;
-    s[S_TLEN] = t_len;
-    s[S_MAXSTEPS] = max_steps;
-    s[S_CAP] = cap;
+  if (threadIdx.x == 0) {
+    state[S_PHASE] = t_len > 0 ? PH_START : PH_DONE;
+    state[S_FRAME] = 0;
+    state[S_DONE] = t_len <= 0;
+    state[S_NTOK] = 0;
+    state[S_GUARD] = 0;
+    state[S_PAR] = 0;
+    state[S_LSTM] = 1;
+    state[S_PQ] = 0;
+    state[S_TLEN] = t_len;
+    state[S_MAXSTEPS] = max_steps;
+    state[S_CAP] = cap;
   }
 }
 
@@ -340,7 +362,19 @@ Weights weights_of(const TdtDev& d) {
   return Weights{d.embed, d.w_ih, d.w_hh, d.proj_w, d.head_w, d.b_ih, d.b_hh, d.proj_b, d.head_b};
 }
 
-constexpr int STEP_G = TDT_PARTIALS;  // workgroups per phase
+// Workgroups per launch: every head row needs a row group (64 per
+// workgroup), every channel a wave (8 per workgroup). BARK_HIP_TDT_GROUPS
+// overrides the default for tuning.
+int groups() {
+  static const int g = [] {
+    if (const char* e = std::getenv("BARK_HIP_TDT_GROUPS")) {
+      const int v = std::atoi(e);
+      if (v * 64 >= NROWS && v * WAVES >= DH && v <= TDT_PARTIALS) return v;
+    }
+    return TDT_PARTIALS;
+  }();
+  return g;
+}
 
 }  // namespace
 
@@ -349,31 +383,23 @@ int tdt_frame_word() { return S_FRAME; }
 int tdt_done_word() { return S_DONE; }
 int tdt_count_word() { return S_NTOK; }
 int tdt_max_steps(int t_len) { return t_len * (10 + 4) + 64; }  // src/tdt.rs:381 (MAX_SYMBOLS = 10)
+long tdt_max_launches(int t_len) { return 4L * tdt_max_steps(t_len) + 4; }
 
 void tdt_begin(const TdtDev& d, int t_len, int cap, hipStream_t st) {
-  const Weights W = weights_of(d);
-  int* next = d.state + S_WORDS;
-  const float4* part = reinterpret_cast<const float4*>(d.partials);
   BARK_LAUNCH(tdt_init_kernel, dim3(1), dim3(64), 0, st, d.state, t_len, tdt_max_steps(t_len), cap);
-  BARK_LAUNCH(tdt_lstm0_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, 1, (const int*)d.state, next, part, d.tokens,
-              d.h, d.c);
-  BARK_LAUNCH(tdt_lstm1_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, (const int*)next, d.h, d.c);
-  BARK_LAUNCH(tdt_proj_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, d.state, (const int*)next, (const float*)d.h,
-              d.dec);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
-void tdt_steps(const TdtDev& d, const float* pooler, int steps, hipStream_t st) {
+const int* tdt_current(const TdtDev& d, long launches) { return d.state + (launches & 1) * S_WORDS; }
+
+void tdt_launches(const TdtDev& d, const float* pooler, int n, long& launches, hipStream_t st) {
   const Weights W = weights_of(d);
-  int* next = d.state + S_WORDS;
+  const int G = groups();
   float4* part = reinterpret_cast<float4*>(d.partials);
-  for (int s = 0; s < steps; ++s) {
-    BARK_LAUNCH(tdt_joint_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, pooler, (const float*)d.dec,
-                (const int*)d.state, part);
-    BARK_LAUNCH(tdt_lstm0_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, 0, (const int*)d.state, next,
-                (const float4*)part, d.tokens, d.h, d.c);
-    BARK_LAUNCH(tdt_lstm1_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, (const int*)next, d.h, d.c);
-    BARK_LAUNCH(tdt_proj_kernel, dim3(STEP_G), dim3(THREADS), 0, st, W, d.state, (const int*)next, (const float*)d.h,
+  for (int i = 0; i < n; ++i, ++launches) {
+    const int* in = d.state + (launches & 1) * S_WORDS;
+    int* out = d.state + ((launches + 1) & 1) * S_WORDS;
+    BARK_LAUNCH(tdt_advance_kernel, dim3(G), dim3(THREADS), 0, st, W, pooler, in, out, part, d.tokens, d.h, d.c,
                 d.dec);
   }
   BARK_HIP_CHECK(hipGetLastError());
