@@ -145,10 +145,14 @@ __device__ void phase_joint(const Weights& W, const Row& row, bool has_row, cons
   if (has_row) {
     const int r = wg + G * (threadIdx.x >> 3);
     const float sc = W.head_b[r] + row.dot(sh.xs, threadIdx.x & 7);
-    if (r < VOCAB)
-      b.ts = sc, b.ti = r;
-    else
-      b.ds = sc, b.di = r;
+    // a row competes only with a score above -inf (NaN never does), as the
+    // reference's `score > best` scan from -inf
+    if (sc > -INFINITY) {
+      if (r < VOCAB)
+        b.ts = sc, b.ti = r;
+      else
+        b.ds = sc, b.di = r;
+    }
   }
   b.wave_reduce(8);
   if ((threadIdx.x & 63) == 0) sh.wave_best[threadIdx.x >> 6] = b;
@@ -172,10 +176,10 @@ __device__ void phase_decide(const float4* part, int G, Lds& sh) {
     }
     b.wave_reduce(1);
     if (threadIdx.x == 0) {
-      // with NaN everywhere no row qualifies: token 0 (the reference's initial
-      // best) and duration 0 keep the control flow in range
+      // no qualifying row: token 0 and duration row 0, i.e. 0 - 8193 (the
+      // reference's initial best; its u32 duration wraps and ends the decode)
       sh.tok = b.ti < VOCAB ? b.ti : 0;
-      sh.dur = (b.di >= VOCAB && b.di < NROWS) ? b.di - VOCAB : 0;
+      sh.dur = (b.di >= VOCAB && b.di < NROWS) ? b.di - VOCAB : -VOCAB;
     }
   }
   __syncthreads();
@@ -295,7 +299,15 @@ __global__ void __launch_bounds__(THREADS) tdt_advance_kernel(Weights W, const f
       phase_decide(part + q * TDT_PARTIALS, G, sh);
       const int tok = sh.tok, dur = sh.dur;
       ++guard;
-      if (tok == BLANK) {
+      if (dur < 0) {  // a wrapped duration moves the frame past any T
+        if (tok != BLANK && wg == 0 && threadIdx.x == 0 && ntok < in[S_CAP]) {
+          tokens[3 * ntok] = (uint32_t)tok;
+          tokens[3 * ntok + 1] = (uint32_t)frame;
+          tokens[3 * ntok + 2] = (uint32_t)dur;
+        }
+        ntok += tok != BLANK;
+        frame = in[S_TLEN];
+      } else if (tok == BLANK) {
         frame += max(dur, 1);
       } else {
         if (wg == 0 && threadIdx.x == 0 && ntok < in[S_CAP]) {

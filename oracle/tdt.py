@@ -6,9 +6,12 @@ Follows TdtDecoder::decode_rayon (src/tdt.rs:374-414) with the pieces it calls:
   lstm_step .... per layer gates = b_ih + b_hh + w_ih x + w_hh h in PyTorch's
                  row order i, f, g, o; c = f c + i g; h = o tanh(c); layer 1
                  takes the new h0 (:179-214);
-  joint ........ x = max(enc + dec, 0); scores = head_w x + head_b; token =
-                 first argmax of rows 0..8192, duration = first argmax of rows
-                 8193..8197 minus 8193 (:217-288);
+  joint ........ x = max(enc + dec, 0) (NaN -> 0, f32::max); scores = head_w x
+                 + head_b; token = first row of the highest score above -inf
+                 among rows 0..8192 (NaN never qualifies; none: 0), duration
+                 likewise over rows 8193..8197 minus 8193 (none: 0 - 8193,
+                 which as a u32 moves the frame past T and ends the loop)
+                 (:217-288);
   loop ......... stop when frame >= T or after T * (10 + 4) + 64 steps; blank:
                  frame += max(dur, 1); token: emit {id, frame, dur}, LSTM step
                  on its embedding, new dec, frame += dur (:386-412).
@@ -57,8 +60,9 @@ class Decoder:
         return self.proj_w @ h1 + self.proj_b
 
     def scores(self, enc, dec):
-        """joint scores of the 8193 token rows and 5 duration rows"""
-        return self.head_w @ np.maximum(enc + dec, 0.0) + self.head_b
+        """joint scores of the 8193 token rows and 5 duration rows; max(x, 0)
+        returns 0 for NaN like Rust's f32::max"""
+        return self.head_w @ np.fmax(enc + dec, 0.0) + self.head_b
 
     def start(self):
         """(h, c, dec) after the start step on the blank embedding"""
@@ -70,8 +74,10 @@ class Decoder:
     def joint(self, enc, dec):
         s = self.scores(enc, dec)
         tok_s, dur_s = s[:VOCAB], s[VOCAB:]
-        tok, dur = int(np.argmax(tok_s)), int(np.argmax(dur_s))
-        return tok, dur, margin(tok_s, tok), margin(dur_s, dur)
+        tok, dur = first_max(tok_s), first_max(dur_s)
+        # no qualifying duration row: row 0, whose u32 duration 0 - 8193 wraps
+        dur = dur if dur is not None else -VOCAB
+        return (tok if tok is not None else 0), dur, margin(tok_s, tok or 0), margin(dur_s, max(dur, 0))
 
     def decode(self, pooler, t_len=None, with_margins=False):
         pooler = np.asarray(pooler, np.float32).astype(np.float64)
@@ -86,6 +92,10 @@ class Decoder:
                 break
             tok, dur, mt, md = self.joint(pooler[frame], dec)
             margins.append((mt, md))
+            if dur < 0:  # the wrapped duration moves the frame past any T
+                if tok != BLANK:
+                    tokens.append((tok, frame, dur % (1 << 32)))
+                break
             if tok == BLANK:
                 frame += max(dur, 1)
             else:
@@ -95,6 +105,16 @@ class Decoder:
                 frame += dur
         out = np.asarray(tokens, np.uint32).reshape(-1, 3)
         return (out, np.asarray(margins).reshape(-1, 2)) if with_margins else out
+
+
+def first_max(scores):
+    """the reference's scan (src/tdt.rs:236-263): the first row with the highest
+    score above -inf; NaN never qualifies; None when no row does"""
+    ok = scores > -np.inf  # False for NaN
+    if not ok.any():
+        return None
+    best = scores[ok].max()
+    return int(np.flatnonzero(ok & (scores == best))[0])
 
 
 def margin(scores, best):

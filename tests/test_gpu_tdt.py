@@ -152,3 +152,21 @@ def test_transcribe_wave_batch(pkg, synth):
         assert sum(len(g) for g in got) > 0
     finally:
         enc.close()
+
+
+def test_tdt_nan_inputs(pkg, synth):
+    """NaN pooler rows (max(x, 0) -> 0) and NaN duration scores (no qualifying
+    row: the wrapped duration ends the decode), as the oracle's reference rules"""
+    print("case tdt nan", flush=True)
+    import test_oracle_tdt as t
+
+    p = synth.pooler(300, 0)
+    p[40:60] = np.nan
+    p[100, :7] = np.nan
+    for kw, src in ((dict(seed=0), None), (dict(seed=0, blank_bias=-5.0), t._NanDurations(synth, seed=0, blank_bias=-5.0))):
+        dec = src if src is not None else synth.SynthTdt(**kw)
+        enc = pkg.HipEncoder.load_with(synth.SynthCheckpoint(seed=1, n_layers=1), 0, 1, decoder=dec)
+        try:
+            np.testing.assert_array_equal(enc.tdt_decode(p), otdt.Decoder(dec).decode(p))
+        finally:
+            enc.close()

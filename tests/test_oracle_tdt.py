@@ -129,3 +129,39 @@ def _decode_without_blank_min(d, pooler):
             dec = d.project(h[1])
         frame += dur
     return np.asarray(out, np.uint32).reshape(-1, 3)
+
+
+class _NanDurations:
+    """SynthTdt with NaN duration biases: no duration row qualifies"""
+
+    def __init__(self, synth, **kw):
+        self.src = synth.SynthTdt(**kw)
+
+    def read(self, name):
+        v = np.array(self.src.read(name), copy=True)
+        if name == "joint.head.bias":
+            v[otdt.VOCAB:] = np.nan
+        return v
+
+
+def test_no_duration_row_ends_the_decode(synth):
+    """the reference's scan keeps duration row 0 when no score beats -inf; its
+    u32 duration 0 - 8193 wraps and moves the frame past T (src/tdt.rs:236-263,
+    287, 396-410): one step, and a token (if any) records the wrapped value"""
+    d = otdt.Decoder(_NanDurations(synth, seed=0, blank_bias=-5.0))
+    toks, margins = d.decode(synth.pooler(50, 0), with_margins=True)
+    assert len(margins) == 1
+    assert toks.shape == (1, 3) and toks[0, 1] == 0 and toks[0, 2] == (1 << 32) - otdt.VOCAB
+    d = otdt.Decoder(_NanDurations(synth, seed=0, blank_bias=50.0))
+    toks, margins = d.decode(synth.pooler(50, 0), with_margins=True)
+    assert len(margins) == 1 and toks.shape == (0, 3)
+
+
+def test_nan_pooler_entries_act_as_zero(synth):
+    """max(enc + dec, 0) gives 0 for NaN as Rust's f32::max (and for -inf)"""
+    d = otdt.Decoder(synth.SynthTdt(seed=0))
+    p = synth.pooler(60, 3)
+    p[10:20] = np.nan
+    q = p.copy()
+    q[10:20] = -np.inf
+    np.testing.assert_array_equal(d.decode(p), d.decode(q))
