@@ -161,6 +161,14 @@ _SIGS = {
         _c.c_int,
         [_c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_size_t, _c.POINTER(_c.c_int32), _c.c_void_p],
     ),
+    "bark_hip_tdt_decode_batch": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_size_t, _c.c_void_p],
+    ),
+    "bark_hip_tdt_decode_batch_device": (
+        _c.c_int,
+        [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_size_t, _c.c_void_p, _c.c_void_p],
+    ),
     "bark_hip_transcribe_wave_batch": (
         _c.c_int,
         [_c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_void_p, _c.c_size_t, _c.c_void_p],
@@ -442,6 +450,22 @@ class HipEncoder:
             )
         )
         return out[: n.value].copy()
+
+    def tdt_decode_batch(self, poolers: Sequence[np.ndarray]) -> list[np.ndarray]:
+        """Greedy TDT decoding of several poolers together (every launch
+        advances all of them); one (n, 3) u32 token array per pooler."""
+        ps = [np.ascontiguousarray(p, dtype=np.float32).reshape(-1, PROJ) for p in poolers]
+        t = np.asarray([p.shape[0] for p in ps], np.int32)
+        flat = np.ascontiguousarray(np.concatenate(ps)) if t.sum() else np.zeros((1, PROJ), np.float32)
+        cap = int(sum(int(k) * 14 + 64 for k in t))
+        out = np.zeros((cap, 3), np.uint32)
+        counts = np.zeros(len(ps), np.int32)
+        _check(lib().bark_hip_tdt_decode_batch(self._h, _ptr(flat), _ptr(t), len(ps), _ptr(out), cap, _ptr(counts)))
+        res, row = [], 0
+        for c in counts:
+            res.append(out[row : row + int(c)].copy())
+            row += int(c)
+        return res
 
     def transcribe_wave_batch(self, waves: Sequence[np.ndarray]) -> list[np.ndarray]:
         """Log-mel, one batched encode and the greedy TDT decode of every 16 kHz

@@ -225,8 +225,7 @@ struct BarkHip {
   // tensors were staged), state, and a pinned copy of the state words
   TdtDev tdt;
   bool has_tdt = false;
-  DevBuf tdt_state, tdt_h, tdt_c, tdt_dec, tdt_part, tdt_tokens, tdt_pooler;
-  int* tdt_host = nullptr;
+  DevBuf tdt_state, tdt_h, tdt_c, tdt_dec, tdt_part, tdt_tokens, tdt_pooler, tdt_params;
 
   void set_mel_filters(const float* filters) {
     constexpr int NB = 257;
@@ -325,10 +324,9 @@ struct BarkHip {
                       &pooler, &dump, &bounds, &tiles, &y2, &y3, &y4, &mel, &subf32,
                       &merges, &attn_lanes, &attn_po, &attn_pml, &mel_window, &mel_twid,
                       &mel_rows, &mel_vals, &mel_ws, &mel_wave, &mel_feat, &tdt_state, &tdt_h,
-                      &tdt_c, &tdt_dec, &tdt_part, &tdt_tokens, &tdt_pooler};
+                      &tdt_c, &tdt_dec, &tdt_part, &tdt_tokens, &tdt_pooler, &tdt_params};
     for (DevBuf* b : bufs)
       if (b->p) (void)hipFree(b->p);
-    if (tdt_host) (void)hipHostFree(tdt_host);
     if (stream) (void)hipStreamDestroy(stream);
   }
 
@@ -539,67 +537,109 @@ struct BarkHip {
     HostLinear hw = linear("joint.head.weight", NR, DH, false);
     tdt.head_w = reinterpret_cast<const half*>(upload(hw.w16.data(), hw.w16.size()));
     tdt.head_b = f32_dev("joint.head.bias", NR);
-    ensure(tdt_state, (size_t)tdt_state_words() * 2 * 4);  // current and next control state
-    ensure(tdt_h, 4 * DH * 4);
-    ensure(tdt_c, 2 * DH * 4);
-    ensure(tdt_dec, DH * 4);
-    ensure(tdt_part, 2 * TDT_PARTIALS * 16);
-    BARK_HIP_CHECK(hipHostMalloc((void**)&tdt_host, (size_t)tdt_state_words() * 4, hipHostMallocDefault));
-    tdt.state = tdt_state.as<int>();
-    tdt.h = tdt_h.as<float>();
-    tdt.c = tdt_c.as<float>();
-    tdt.dec = tdt_dec.as<float>();
-    tdt.partials = tdt_part.as<float>();
   }
 
-  // Greedy TDT decoding of a device pooler (t_len x 640 f32) on `st`
-  // (TdtDecoder::decode, src/tdt.rs:318-414; GpuTdtDecoder::decode_async,
-  // src/tdt_gpu.rs:206-300). Launches are queued in chunks; after each chunk
-  // only the control state comes back, and decoding ends when the device sets
-  // `done`. Returns the number of tokens; their {id, frame, dur} words stay in
-  // tdt_tokens.
-  int tdt_decode(const float* d_pooler, int t_len, hipStream_t st) {
+  // Greedy TDT decoding of `batch` device poolers (TdtDecoder::decode,
+  // src/tdt.rs:318-414; GpuTdtDecoder::decode_async, src/tdt_gpu.rs:206-300):
+  // utterance u has t[u] frames of 640 f32 from row rows[u] of d_pooler. Every
+  // launch advances all utterances; launches are queued in chunks, after each
+  // chunk only the control states come back, and decoding ends when every
+  // utterance is done. Returns the token counts; utterance u's {id, frame, dur}
+  // records start at record first[u] of tdt_tokens.
+  std::vector<int> tdt_decode(const float* d_pooler, const int* rows, const int* t, int batch,
+                              std::vector<size_t>& first, hipStream_t st) {
     BARK_REQUIRE(finalized, "decode before finalize");
     BARK_REQUIRE(has_tdt, "no TDT decoder tensors were set before finalize");
-    BARK_REQUIRE(t_len >= 0 && t_len <= (1 << 24), "t_len out of range");
-    if (t_len == 0) return 0;  // src/tdt_gpu.rs:211-216
-    const int max_steps = tdt_max_steps(t_len);
-    const long max_launches = tdt_max_launches(t_len);
-    ensure(tdt_tokens, (size_t)max_steps * 12);
+    BARK_REQUIRE(batch >= 1 && batch <= 65535, "batch out of range");
+    std::vector<int> params(4 * (size_t)batch);
+    first.assign(batch, 0);
+    size_t records = 0;
+    long max_launches = 0;
+    int max_t = 0;
+    for (int u = 0; u < batch; ++u) {
+      BARK_REQUIRE(t[u] >= 0 && t[u] <= (1 << 24), "t_len out of range");
+      BARK_REQUIRE(t[u] == 0 || d_pooler, "null pooler");
+      const int cap = t[u] ? tdt_max_steps(t[u]) : 0;
+      params[4 * u] = t[u];
+      params[4 * u + 1] = rows[u];
+      params[4 * u + 2] = (int)records;
+      params[4 * u + 3] = cap;
+      first[u] = records;
+      records += (size_t)cap;
+      BARK_REQUIRE(records < (1u << 31), "too many frames for one decode");
+      if (t[u]) max_launches = std::max(max_launches, tdt_max_launches(t[u]));
+      max_t = std::max(max_t, t[u]);
+    }
+    std::vector<int> counts(batch, 0);
+    if (max_launches == 0) return counts;  // every pooler empty (src/tdt_gpu.rs:211-216)
+    const size_t words = (size_t)tdt_state_words();
+    ensure(tdt_state, (size_t)batch * 2 * words * 4);
+    ensure(tdt_h, (size_t)batch * TDT_H_BYTES);
+    ensure(tdt_c, (size_t)batch * TDT_C_BYTES);
+    ensure(tdt_dec, (size_t)batch * TDT_DEC_BYTES);
+    ensure(tdt_part, (size_t)batch * TDT_PART_BYTES);
+    ensure(tdt_params, params.size() * 4);
+    ensure(tdt_tokens, std::max<size_t>(records, 1) * 12);
     TdtDev d = tdt;
+    d.state = tdt_state.as<int>();
+    d.h = tdt_h.as<float>();
+    d.c = tdt_c.as<float>();
+    d.dec = tdt_dec.as<float>();
+    d.partials = tdt_part.as<float>();
     d.tokens = tdt_tokens.as<uint32_t>();
+    BARK_HIP_CHECK(hipMemcpyAsync(tdt_params.p, params.data(), params.size() * 4, hipMemcpyHostToDevice, st));
+    tdt_begin(d, tdt_params.as<int>(), batch, st);
     // per token step: joint head, both LSTM layers and the projection (f16)
     const double step_bytes = 2.0 * 640 * (8198 + 4 * 2560 + 640);
-    const size_t words = (size_t)tdt_state_words() * 4;
-    tdt_begin(d, t_len, max_steps, st);
-    long launches = 0;
-    long chunk = std::max(16, t_len / 2);
+    std::vector<int> host((size_t)batch * 2 * words);
+    long launches = 0, chunk = std::max(16, max_t / 2);
+    bool all_done = false;
     while (true) {
       const int n = (int)std::min(chunk, max_launches - launches);
-      prof.run("tdt_decode", 0, step_bytes * n / 4, st, [&] { tdt_launches(d, d_pooler, n, launches, st); });
-      BARK_HIP_CHECK(
-          hipMemcpyAsync(tdt_host, tdt_current(d, launches), words, hipMemcpyDeviceToHost, st));
+      prof.run("tdt_decode", 0, step_bytes * n / 4 * batch, st,
+               [&] { tdt_launches(d, d_pooler, batch, n, launches, st); });
+      BARK_HIP_CHECK(hipMemcpyAsync(host.data(), d.state, host.size() * 4, hipMemcpyDeviceToHost, st));
       BARK_HIP_CHECK(hipStreamSynchronize(st));
-      if (tdt_host[tdt_done_word()] || launches >= max_launches) break;
-      // the rest at the rate seen so far (launches per frame), plus a margin
-      const int frame = tdt_host[tdt_frame_word()];
-      const double rate = (double)launches / std::max(frame, 1);
-      chunk = std::max(16L, (long)(rate * (t_len - frame)) + 8);
+      // the rest at the rate seen so far (launches per frame), for the utterance furthest behind
+      all_done = true;
+      long rest = 0;
+      for (int u = 0; u < batch; ++u) {
+        const int* cur = host.data() + (tdt_current(d, launches, u) - d.state);
+        if (cur[tdt_done_word()]) continue;
+        all_done = false;
+        const int frame = cur[tdt_frame_word()];
+        rest = std::max(rest, (long)((double)launches / std::max(frame, 1) * (t[u] - frame)));
+      }
+      if (all_done || launches >= max_launches) break;
+      chunk = std::max(16L, rest + 8);
     }
-    BARK_REQUIRE(tdt_host[tdt_done_word()], "TDT decoding did not finish within the step guard");
-    return tdt_host[tdt_count_word()];
+    BARK_REQUIRE(all_done, "TDT decoding did not finish within the step guard");
+    for (int u = 0; u < batch; ++u)
+      counts[u] = (host.data() + (tdt_current(d, launches, u) - d.state))[tdt_count_word()];
+    return counts;
   }
 
-  void tdt_decode_copy(const float* d_pooler, int t_len, uint32_t* tokens, size_t cap, int32_t* n_tokens,
-                       hipStream_t st) {
-    const int n = tdt_decode(d_pooler, t_len, st);
-    if (n_tokens) *n_tokens = n;
-    BARK_REQUIRE((size_t)n <= cap, "token buffer too small: " + std::to_string(n) + " tokens");
-    if (n > 0) {
-      BARK_REQUIRE(tokens, "null token buffer");
-      BARK_HIP_CHECK(hipMemcpyAsync(tokens, tdt_tokens.p, (size_t)n * 12, hipMemcpyDeviceToHost, st));
-      BARK_HIP_CHECK(hipStreamSynchronize(st));
+  // decode and copy every utterance's records to `tokens` back to back
+  void tdt_decode_copy(const float* d_pooler, const int* rows, const int* t, int batch, uint32_t* tokens, size_t cap,
+                       int32_t* n_tokens, hipStream_t st) {
+    std::vector<size_t> first;
+    const std::vector<int> counts = tdt_decode(d_pooler, rows, t, batch, first, st);
+    size_t total = 0;
+    for (int u = 0; u < batch; ++u) {
+      if (n_tokens) n_tokens[u] = counts[u];
+      total += (size_t)counts[u];
     }
+    BARK_REQUIRE(total <= cap, "token buffer too small: " + std::to_string(total) + " tokens");
+    size_t off = 0;
+    for (int u = 0; u < batch; ++u) {
+      if (counts[u] > 0) {
+        BARK_REQUIRE(tokens, "null token buffer");
+        BARK_HIP_CHECK(hipMemcpyAsync(tokens + 3 * off, tdt_tokens.as<uint32_t>() + 3 * first[u],
+                                      (size_t)counts[u] * 12, hipMemcpyDeviceToHost, st));
+      }
+      off += (size_t)counts[u];
+    }
+    BARK_HIP_CHECK(hipStreamSynchronize(st));
   }
 
   // ------------------------------------------------------- position table --
@@ -1048,18 +1088,12 @@ struct BarkHip {
     }
     std::vector<std::pair<int, int>> rows;
     encode_mel_batch(mel.as<float>(), true, frames.data(), valid.data(), batch, t_out, nullptr, true, 0, st, &rows);
-    size_t off = 0;
+    std::vector<int> r0(batch), tl(batch);
     for (int i = 0; i < batch; ++i) {
-      const int n = tdt_decode(pooler.as<float>() + (size_t)rows[i].first * PROJ, rows[i].second, st);
-      n_tokens[i] = n;
-      BARK_REQUIRE(off + (size_t)n <= cap, "token buffer too small");
-      if (n > 0) {
-        BARK_REQUIRE(tokens, "null token buffer");
-        BARK_HIP_CHECK(hipMemcpyAsync(tokens + 3 * off, tdt_tokens.p, (size_t)n * 12, hipMemcpyDeviceToHost, st));
-        BARK_HIP_CHECK(hipStreamSynchronize(st));
-      }
-      off += (size_t)n;
+      r0[i] = rows[i].first;
+      tl[i] = rows[i].second;
     }
+    tdt_decode_copy(pooler.as<float>(), r0.data(), tl.data(), batch, tokens, cap, n_tokens, st);
   }
 
   void encode_sub(const float* sub_rows, int t, int dump_layer, float* out_pooler,
@@ -1395,28 +1429,53 @@ int bark_hip_encode_wave_batch(BarkHip* h, const float* waves, const int64_t* n_
 
 int bark_hip_tdt_decode(BarkHip* h, const float* pooler, int32_t t_len, uint32_t* tokens, size_t cap,
                         int32_t* n_tokens) {
-  return guarded([&] {
-    BARK_REQUIRE(h && (pooler || t_len == 0), "null argument");
-    std::lock_guard<std::mutex> lk(h->mu);
-    BARK_HIP_CHECK(hipSetDevice(h->device));
-    BARK_REQUIRE(t_len >= 0 && t_len <= (1 << 24), "t_len out of range");
-    if (t_len > 0) {
-      h->ensure(h->tdt_pooler, (size_t)t_len * 640 * 4);
-      BARK_HIP_CHECK(hipMemcpyAsync(h->tdt_pooler.p, pooler, (size_t)t_len * 640 * 4, hipMemcpyHostToDevice,
-                                    h->stream));
-    }
-    h->tdt_decode_copy(h->tdt_pooler.as<float>(), t_len, tokens, cap, n_tokens, h->stream);
-  });
+  return bark_hip_tdt_decode_batch(h, pooler, &t_len, 1, tokens, cap, n_tokens);
 }
 
 int bark_hip_tdt_decode_device(BarkHip* h, const float* d_pooler, int32_t t_len, uint32_t* tokens, size_t cap,
                                int32_t* n_tokens, void* stream) {
+  return bark_hip_tdt_decode_batch_device(h, d_pooler, &t_len, 1, tokens, cap, n_tokens, stream);
+}
+
+int bark_hip_tdt_decode_batch(BarkHip* h, const float* pooler, const int32_t* t_lens, int32_t batch, uint32_t* tokens,
+                              size_t cap, int32_t* n_tokens) {
   return guarded([&] {
-    BARK_REQUIRE(h && (d_pooler || t_len == 0), "null argument");
+    BARK_REQUIRE(h && t_lens && batch >= 1, "null argument");
+    std::lock_guard<std::mutex> lk(h->mu);
+    BARK_HIP_CHECK(hipSetDevice(h->device));
+    std::vector<int> rows(batch);
+    size_t total = 0;
+    for (int u = 0; u < batch; ++u) {
+      BARK_REQUIRE(t_lens[u] >= 0 && t_lens[u] <= (1 << 24), "t_len out of range");
+      rows[u] = (int)total;
+      total += (size_t)t_lens[u];
+      BARK_REQUIRE(total < (1u << 31), "too many frames");
+    }
+    BARK_REQUIRE(pooler || total == 0, "null pooler");
+    if (total > 0) {
+      h->ensure(h->tdt_pooler, total * 640 * 4);
+      BARK_HIP_CHECK(hipMemcpyAsync(h->tdt_pooler.p, pooler, total * 640 * 4, hipMemcpyHostToDevice, h->stream));
+    }
+    h->tdt_decode_copy(h->tdt_pooler.as<float>(), rows.data(), t_lens, batch, tokens, cap, n_tokens, h->stream);
+  });
+}
+
+int bark_hip_tdt_decode_batch_device(BarkHip* h, const float* d_pooler, const int32_t* t_lens, int32_t batch,
+                                     uint32_t* tokens, size_t cap, int32_t* n_tokens, void* stream) {
+  return guarded([&] {
+    BARK_REQUIRE(h && t_lens && batch >= 1, "null argument");
     std::lock_guard<std::mutex> lk(h->mu);
     BARK_HIP_CHECK(hipSetDevice(h->device));
     hipStream_t st = stream ? static_cast<hipStream_t>(stream) : h->stream;
-    h->tdt_decode_copy(d_pooler, t_len, tokens, cap, n_tokens, st);
+    std::vector<int> rows(batch);
+    size_t total = 0;
+    for (int u = 0; u < batch; ++u) {
+      BARK_REQUIRE(t_lens[u] >= 0 && t_lens[u] <= (1 << 24), "t_len out of range");
+      rows[u] = (int)total;
+      total += (size_t)t_lens[u];
+      BARK_REQUIRE(total < (1u << 31), "too many frames");
+    }
+    h->tdt_decode_copy(d_pooler, rows.data(), t_lens, batch, tokens, cap, n_tokens, st);
   });
 }
 

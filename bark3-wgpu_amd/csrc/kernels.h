@@ -171,10 +171,10 @@ void mel_features(const float* wave, long n_samples, const MelTables& tb, void* 
 // ---------------------------------------------------------------- TDT --
 // Device buffers of the greedy TDT decoder (tdt.hip): embedding (8193 x 640)
 // and biases f32; LSTM (2 layers x 2560 x 640, ih and hh), projection
-// (640 x 640) and joint head (8198 x 640) f16; state words (the current
-// control state, then the next one); h (2 layers x 2
-// buffers x 640), c (2 x 640), dec (640), joint partials (2 x 256 float4),
-// tokens (cap x {id, frame, dur}).
+// (640 x 640) and joint head (8198 x 640) f16; then, per utterance of a batch,
+// two control-state buffers, h (2 layers x 2 buffers x 640), c (2 x 640), dec
+// (640) and joint partials (2 x 256 float4); token records {id, frame, dur}
+// for the whole batch.
 struct TdtDev {
   const float* embed = nullptr;
   const half *w_ih = nullptr, *w_hh = nullptr, *proj_w = nullptr, *head_w = nullptr;
@@ -184,19 +184,23 @@ struct TdtDev {
   uint32_t* tokens = nullptr;
 };
 constexpr int TDT_PARTIALS = 256;  // joint partials per set (the largest grid); two sets
-int tdt_state_words();  // words of one control state (the buffer holds two)
-int tdt_frame_word();  // index of the frame pointer among the state words
-int tdt_done_word();   // index of the `done` flag
-int tdt_count_word();  // index of the emitted-token count
+// bytes per utterance of the batched buffers
+constexpr size_t TDT_H_BYTES = 4 * 640 * 4, TDT_C_BYTES = 2 * 640 * 4, TDT_DEC_BYTES = 640 * 4,
+                 TDT_PART_BYTES = 2 * TDT_PARTIALS * 16;
+int tdt_state_words();  // words of one control state (two buffers per utterance)
+int tdt_frame_word();   // index of the frame pointer among the state words
+int tdt_done_word();    // index of the `done` flag
+int tdt_count_word();   // index of the emitted-token count
 int tdt_max_steps(int t_len);
 long tdt_max_launches(int t_len);  // launches after which `done` is certain
-// reset the control state for a pooler of t_len frames (the start step pending)
-void tdt_begin(const TdtDev& d, int t_len, int cap, hipStream_t st);
-// queue n launches, each running the phase the control state names; `launches`
-// counts them from tdt_begin (it selects the state buffer)
-void tdt_launches(const TdtDev& d, const float* pooler, int n, long& launches, hipStream_t st);
-// the state buffer that holds the control state after `launches` launches
-const int* tdt_current(const TdtDev& d, long launches);
+// reset the control states of `batch` utterances; d_params (device) holds per
+// utterance {t_len, first pooler row, first token record, record capacity}
+void tdt_begin(const TdtDev& d, const int* d_params, int batch, hipStream_t st);
+// queue n launches, each advancing every utterance by the phase its control
+// state names; `launches` counts them from tdt_begin (it selects the buffer)
+void tdt_launches(const TdtDev& d, const float* pooler, int batch, int n, long& launches, hipStream_t st);
+// utterance u's control state after `launches` launches
+const int* tdt_current(const TdtDev& d, long launches, int u);
 
 // ---------------------------------------------------------- safetensors --
 // One tensor entry of a safetensors header (ingest.hip); begin / end are

@@ -54,7 +54,8 @@ constexpr int ROW_LOADS = DH / 8 / 8;  // 16-byte loads per lane per row (10)
 constexpr int NONE = 0x7fffffff;
 
 // state words (int32)
-enum { S_PHASE, S_FRAME, S_DONE, S_NTOK, S_GUARD, S_PAR, S_LSTM, S_PQ, S_TLEN, S_MAXSTEPS, S_CAP, S_WORDS };
+enum { S_PHASE, S_FRAME, S_DONE, S_NTOK, S_GUARD, S_PAR, S_LSTM, S_PQ, S_TLEN, S_MAXSTEPS, S_CAP, S_ROW0, S_TOK0,
+       S_WORDS };
 typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
 __device__ inline float2 halves(uint32_t u) {
@@ -260,11 +261,29 @@ __device__ void phase_proj(const Weights& W, const float* h1, float* dec, int G,
 // A run of blanks costs one launch per step; a token step four.
 enum { PH_START, PH_L1, PH_PROJ, PH_JOINT, PH_DECIDE, PH_DONE };
 
-__global__ void __launch_bounds__(THREADS) tdt_advance_kernel(Weights W, const float* pooler, const int* in,
-                                                              int* out, float4* part, uint32_t* tokens, float* h,
-                                                              float* c, float* dec) {
+__host__ __device__ inline int tdt_max_steps_of(int t_len) { return t_len * (10 + 4) + 64; }  // src/tdt.rs:381
+
+
+// Utterance b = blockIdx.y of a batch: its control state, h, c, dec, partials
+// and token records live at fixed strides; its pooler rows start at row
+// S_ROW0 of `pooler` and its token records at record S_TOK0.
+__global__ void __launch_bounds__(THREADS) tdt_advance_kernel(Weights W, const float* pooler, const int* in_all,
+                                                              int* out_all, float4* part_all, uint32_t* tokens,
+                                                              float* h_all, float* c_all, float* dec_all) {
   __shared__ Lds sh;
-  const int G = gridDim.x, wg = blockIdx.x;
+  const int G = gridDim.x, wg = blockIdx.x, u = blockIdx.y;
+  const int* in = in_all + (size_t)u * 2 * S_WORDS;
+  int* out = out_all + (size_t)u * 2 * S_WORDS;
+  float4* part = part_all + (size_t)u * 2 * TDT_PARTIALS;
+  float* h = h_all + (size_t)u * 4 * DH;
+  float* c = c_all + (size_t)u * 2 * DH;
+  float* dec = dec_all + (size_t)u * DH;
+  if (in[S_PHASE] == PH_DONE) {  // keep the state current in both buffers
+    if (wg == 0 && threadIdx.x < S_WORDS) out[threadIdx.x] = in[threadIdx.x];
+    return;
+  }
+  pooler += (size_t)in[S_ROW0] * DH;
+  tokens += (size_t)in[S_TOK0] * 3;
   const int phase = in[S_PHASE];
   // the control state this launch leaves (workgroup 0 writes it at the end)
   int frame = in[S_FRAME], ntok = in[S_NTOK], guard = in[S_GUARD], lstm = in[S_LSTM], par = in[S_PAR];
@@ -354,36 +373,43 @@ __global__ void __launch_bounds__(THREADS) tdt_advance_kernel(Weights W, const f
   }
 }
 
-__global__ void tdt_init_kernel(int* state, int t_len, int max_steps, int cap) {
-  if (threadIdx.x == 0) {
-    state[S_PHASE] = t_len > 0 ? PH_START : PH_DONE;
-    state[S_FRAME] = 0;
-    state[S_DONE] = t_len <= 0;
-    state[S_NTOK] = 0;
-    state[S_GUARD] = 0;
-    state[S_PAR] = 0;
-    state[S_LSTM] = 1;
-    state[S_PQ] = 0;
-    state[S_TLEN] = t_len;
-    state[S_MAXSTEPS] = max_steps;
-    state[S_CAP] = cap;
-  }
+// per utterance: {t_len, pooler row, first token record, record capacity}
+__global__ void tdt_init_kernel(int* state_all, const int* params, int batch) {
+  const int u = blockIdx.x * blockDim.x + threadIdx.x;
+  if (u >= batch) return;
+  int* state = state_all + (size_t)u * 2 * S_WORDS;  // the first buffer of the pair
+  const int t_len = params[4 * u];
+  state[S_PHASE] = t_len > 0 ? PH_START : PH_DONE;
+  state[S_FRAME] = 0;
+  state[S_DONE] = t_len <= 0;
+  state[S_NTOK] = 0;
+  state[S_GUARD] = 0;
+  state[S_PAR] = 0;
+  state[S_LSTM] = 1;
+  state[S_PQ] = 0;
+  state[S_TLEN] = t_len;
+  state[S_MAXSTEPS] = tdt_max_steps_of(t_len);
+  state[S_CAP] = params[4 * u + 3];
+  state[S_ROW0] = params[4 * u + 1];
+  state[S_TOK0] = params[4 * u + 2];
 }
 
 Weights weights_of(const TdtDev& d) {
   return Weights{d.embed, d.w_ih, d.w_hh, d.proj_w, d.head_w, d.b_ih, d.b_hh, d.proj_b, d.head_b};
 }
 
-// Workgroups per launch: every head row needs a row group (64 per
-// workgroup), every channel a wave (8 per workgroup). BARK_HIP_TDT_GROUPS
-// overrides the default for tuning.
+// Workgroups per utterance and launch: every head row needs a row group (64
+// per workgroup), every channel a wave (8 per workgroup), so at least 129.
+// 160 measured best (one utterance: 129-256 within noise; a batch of 8 at
+// T = 2207: 43 ms with 160, 57 ms with 129, 60 ms with 256).
+// BARK_HIP_TDT_GROUPS overrides it for tuning.
 int groups() {
   static const int g = [] {
     if (const char* e = std::getenv("BARK_HIP_TDT_GROUPS")) {
       const int v = std::atoi(e);
       if (v * 64 >= NROWS && v * WAVES >= DH && v <= TDT_PARTIALS) return v;
     }
-    return TDT_PARTIALS;
+    return 160;
   }();
   return g;
 }
@@ -394,25 +420,27 @@ int tdt_state_words() { return S_WORDS; }
 int tdt_frame_word() { return S_FRAME; }
 int tdt_done_word() { return S_DONE; }
 int tdt_count_word() { return S_NTOK; }
-int tdt_max_steps(int t_len) { return t_len * (10 + 4) + 64; }  // src/tdt.rs:381 (MAX_SYMBOLS = 10)
+int tdt_max_steps(int t_len) { return tdt_max_steps_of(t_len); }  // MAX_SYMBOLS = 10
 long tdt_max_launches(int t_len) { return 4L * tdt_max_steps(t_len) + 4; }
 
-void tdt_begin(const TdtDev& d, int t_len, int cap, hipStream_t st) {
-  BARK_LAUNCH(tdt_init_kernel, dim3(1), dim3(64), 0, st, d.state, t_len, tdt_max_steps(t_len), cap);
+void tdt_begin(const TdtDev& d, const int* d_params, int batch, hipStream_t st) {
+  BARK_LAUNCH(tdt_init_kernel, dim3((batch + 63) / 64), dim3(64), 0, st, d.state, d_params, batch);
   BARK_HIP_CHECK(hipGetLastError());
 }
 
-const int* tdt_current(const TdtDev& d, long launches) { return d.state + (launches & 1) * S_WORDS; }
+const int* tdt_current(const TdtDev& d, long launches, int u) {
+  return d.state + (size_t)u * 2 * S_WORDS + (launches & 1) * S_WORDS;
+}
 
-void tdt_launches(const TdtDev& d, const float* pooler, int n, long& launches, hipStream_t st) {
+void tdt_launches(const TdtDev& d, const float* pooler, int batch, int n, long& launches, hipStream_t st) {
   const Weights W = weights_of(d);
   const int G = groups();
   float4* part = reinterpret_cast<float4*>(d.partials);
   for (int i = 0; i < n; ++i, ++launches) {
     const int* in = d.state + (launches & 1) * S_WORDS;
     int* out = d.state + ((launches + 1) & 1) * S_WORDS;
-    BARK_LAUNCH(tdt_advance_kernel, dim3(G), dim3(THREADS), 0, st, W, pooler, in, out, part, d.tokens, d.h, d.c,
-                d.dec);
+    BARK_LAUNCH(tdt_advance_kernel, dim3(G, batch), dim3(THREADS), 0, st, W, pooler, in, out, part, d.tokens, d.h,
+                d.c, d.dec);
   }
   BARK_HIP_CHECK(hipGetLastError());
 }

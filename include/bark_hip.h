@@ -140,10 +140,25 @@ int bark_hip_tdt_decode(BarkHip *h, const float *pooler, int32_t t_len, uint32_t
 int bark_hip_tdt_decode_device(BarkHip *h, const float *d_pooler, int32_t t_len, uint32_t *tokens,
                                size_t cap, int32_t *n_tokens, void *stream);
 
+/* Batched form (utterances decoded together: every launch advances all of
+ * them, so a batch costs about as many launches as its longest member): the
+ * poolers of `batch` utterances back to back, t_lens[u] rows each (the layout
+ * bark_hip_encode_mel_batch writes). n_tokens[u] receives utterance u's count;
+ * tokens receives every utterance's triples back to back in order; cap counts
+ * triples (sum of t_lens[u] * 14 + 64 always suffices). Chunked transcription
+ * (src/inference.rs:311-326) decodes its chunks one after another; the result
+ * per chunk is the same. */
+int bark_hip_tdt_decode_batch(BarkHip *h, const float *pooler, const int32_t *t_lens, int32_t batch,
+                              uint32_t *tokens, size_t cap, int32_t *n_tokens);
+/* Device-pointer form of bark_hip_tdt_decode_batch, queued on `stream`. */
+int bark_hip_tdt_decode_batch_device(BarkHip *h, const float *d_pooler, const int32_t *t_lens,
+                                     int32_t batch, uint32_t *tokens, size_t cap, int32_t *n_tokens,
+                                     void *stream);
+
 /* Transcription up to the tokens (AsrInference::transcribe's mel -> encoder
  * -> decoder, src/transcription.rs:56-224, over the VAD chunks of
  * src/inference.rs:298-386): log-mel of each 16 kHz wave, one batched encode,
- * and the greedy TDT decode of each wave's pooler in device memory (the pooler
+ * and one batched greedy TDT decode of the waves' poolers in device memory (the pooler
  * never leaves the device, as with the reference's pooler_buf,
  * src/transcription.rs:200-209). t_out[i] (may be NULL) receives wave i's T;
  * n_tokens[i] its token count; tokens receives every wave's {id, frame, dur}

@@ -170,3 +170,16 @@ def test_tdt_nan_inputs(pkg, synth):
             np.testing.assert_array_equal(enc.tdt_decode(p), otdt.Decoder(dec).decode(p))
         finally:
             enc.close()
+
+
+def test_tdt_decode_batch(base, synth):
+    """utterances decoded together (every launch advances all of them) give
+    each utterance's own tokens, empty and one-frame poolers included"""
+    print("case tdt batch", flush=True)
+    ps = [synth.pooler(300, 1), synth.pooler(1000, 2), np.zeros((0, 640), np.float32), synth.pooler(7, 3),
+          synth.pooler(1, 4)]
+    got = base.tdt_decode_batch(ps)
+    assert len(got) == len(ps)
+    for g, p in zip(got, ps):
+        np.testing.assert_array_equal(g, base.tdt_decode(p))
+    np.testing.assert_array_equal(got[1], oracle(synth, {"seed": 0}, 1000, 2))
