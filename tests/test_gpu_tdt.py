@@ -183,3 +183,37 @@ def test_tdt_decode_batch(base, synth):
     for g, p in zip(got, ps):
         np.testing.assert_array_equal(g, base.tdt_decode(p))
     np.testing.assert_array_equal(got[1], oracle(synth, {"seed": 0}, 1000, 2))
+
+
+def test_transcribe_vs_cpu_oracles(pkg, synth):
+    """wave -> tokens on the GPU equals the CPU oracles chained (numpy log-mel,
+    the C encoder restatement, the numpy TDT decode) on a 3 s wave; the
+    oracle's smallest decision margin is checked to exceed the encoder's
+    f16 rounding, so equality is expected"""
+    import importlib
+
+    import oracle
+    from oracle import mel as omel
+
+    print("case tdt transcribe vs oracles", flush=True)
+    src = synth.SynthCheckpoint(seed=3, n_layers=2, style="rich", lowbit=True)
+    dec = synth.SynthTdt(seed=0, blank_bias=1.5)
+    enc = pkg.HipEncoder.load_with(src, 0, 2, decoder=dec)
+    try:
+        filters = importlib.import_module("bark3_wgpu_amd.mel").slaney_mel_filters()
+        enc.set_mel_filters(filters)
+        rng = np.random.default_rng(11)
+        n = 48000
+        t = np.arange(n) / 16000.0
+        wave = (0.3 * np.sin(2 * np.pi * (220 + 300 * t) * t) + 0.05 * rng.standard_normal(n)).astype(np.float32)
+        got = enc.transcribe_wave_batch([wave])[0]
+    finally:
+        enc.close()
+    feats, frames, valid = omel.features(wave, filters)
+    sub = oracle.subsample(src, feats, valid)
+    T = pkg.conv_len(pkg.conv_len(pkg.conv_len(frames)))
+    pooler = oracle.Encoder(src, 2).encode(sub, T)
+    want, margins = otdt.Decoder(dec).decode(pooler, with_margins=True)
+    assert margins.min() > 2e-3, f"oracle decision margin {margins.min():.2e} too small for this check"
+    assert len(want) > 0
+    np.testing.assert_array_equal(got, want)
