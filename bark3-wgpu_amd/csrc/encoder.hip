@@ -463,10 +463,13 @@ struct BarkHip {
       L.ff2b = to_device(linear(p + "feed_forward2.linear2.weight", 1024, 4096, true));
       L.pw1 = to_device(interleave_glu(linear(p + "conv.pointwise_conv1.weight", 2048, 1024, true)));
       L.pw2 = to_device(linear(p + "conv.pointwise_conv2.weight", 1024, 1024, true));
-      {  // depthwise weights as f16-rounded values (the reference stores f16)
+      {  // depthwise weights as f16-rounded values (the reference stores f16),
+         // tap-major [9][1024] so a thread's 4 channels of one tap are one load
         auto dw = vec_f32(p + "conv.depthwise_conv.weight", 1024 * 9);
-        for (auto& v : dw) v = f16_bits_to_f32(f32_to_f16_bits(v));
-        L.dw = upload(dw.data(), dw.size());
+        std::vector<float> tap(dw.size());
+        for (int c = 0; c < 1024; ++c)
+          for (int i = 0; i < 9; ++i) tap[(size_t)i * 1024 + c] = f16_bits_to_f32(f32_to_f16_bits(dw[(size_t)c * 9 + i]));
+        L.dw = upload(tap.data(), tap.size());
       }
       {  // BatchNorm fold a = w/sqrt(var+1e-5), b = bias - mean*a (src/encoder.rs:546-557)
         auto w = vec_f32(p + "conv.norm.weight", 1024), b = vec_f32(p + "conv.norm.bias", 1024);

@@ -134,7 +134,8 @@ void layer_norm2(const float* x, const float* wa, const float* ba, float* y32,
                  const ResidIn& res = ResidIn());
 // x += res in place (rows x 1024).
 void apply_residual(float* x, int rows, const ResidIn& res, hipStream_t stream);
-// out = f16(silu(BN(dwconv9(g)))) with per-row [start, end) frame bounds.
+// out = f16(silu(BN(dwconv9(g)))) with per-row [start, end) frame bounds;
+// dw is tap-major [9][1024].
 void dwconv_bn_silu(const float* g, const float* dw, const float* bn_a, const float* bn_b,
                     const int2* bounds, half* out, int rows, hipStream_t stream);
 void f32_to_f16(const float* x, half* y, size_t n, hipStream_t stream);

@@ -123,7 +123,10 @@ __global__ void __launch_bounds__(256) ln2_kernel(const float* x, const float* w
 // a difference of an ulp per tap). A thread owns 4 consecutive channels
 // (float4 loads) and DW_ROWS consecutive rows, reading its (DW_ROWS + 8)-row
 // window once; a wave covers 256 channels, a workgroup 4 row groups. Row
-// groups whose windows lie inside their sequences skip the tap masks.
+// groups whose windows lie inside their sequences skip the tap masks. The
+// weights are tap-major, one float4 per tap (36 scalar loads per thread in
+// channel-major order cost 6 % of the kernel); 2 and 8 rows per thread
+// measured slower than 4.
 constexpr int DW_ROWS = 4;
 
 __global__ void __launch_bounds__(256) dwconv_kernel(const float* g, const float* dw,
@@ -134,9 +137,11 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const float* g, const float
   if (r0 >= rows) return;
   float w[4][9];
 #pragma unroll
-  for (int e = 0; e < 4; ++e)
+  for (int i = 0; i < 9; ++i) {  // dw is tap-major [9][1024]
+    const floatx4 t = *reinterpret_cast<const floatx4*>(dw + i * HIDDEN + c);
 #pragma unroll
-    for (int i = 0; i < 9; ++i) w[e][i] = dw[(c + e) * 9 + i];
+    for (int e = 0; e < 4; ++e) w[e][i] = t[e];
+  }
   const floatx4 a = *reinterpret_cast<const floatx4*>(bn_a + c);
   const floatx4 b = *reinterpret_cast<const floatx4*>(bn_b + c);
   floatx4 win[DW_ROWS + 8];
