@@ -1,11 +1,14 @@
 /*
- * bark_hip — C ABI of the MI355X (gfx950) Conformer encoder backend.
+ * bark_hip — C ABI of the MI355X (gfx950) Conformer encoder backend, with the
+ * log-mel front end and the greedy TDT decoder on either side of it.
  *
  * The reference (eclipse005/bark3-wgpu, Rust) drives its GPU encoder through
- * `AsrInference::load` -> `Encoder::load_with` -> `Encoder::encode[_pre]` and
- * its conv front end through `SubGpu::run`. These entry points are what a
- * `Backend::Hip` arm binds over FFI in place of those calls (see
- * INTEGRATION.md for the Rust `extern "C"` block).
+ * `AsrInference::load` -> `Encoder::load_with` -> `Encoder::encode[_pre]`, its
+ * conv front end through `SubGpu::run`, its features through
+ * `MelFrontend::compute` and its decoder through `TdtDecoder::decode` /
+ * `GpuTdtDecoder::decode_async`. These entry points are what a `Backend::Hip`
+ * arm binds over FFI in place of those calls, through a Rust `extern "C"`
+ * block that declares them as below.
  *
  * Conventions
  *  - Every function returns 0 on success and a negative code on error; the
