@@ -123,6 +123,7 @@ _SIGS = {
     ),
     "bark_hip_set_lut4": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_void_p, _c.c_void_p, _c.c_int64, _c.c_int64]),
     "bark_hip_load_safetensors": (_c.c_int, [_c.c_void_p, _c.c_char_p]),
+    "bark_hip_probe": (_c.c_int, [_c.c_char_p, _c.c_char_p, _c.c_size_t]),
     "bark_hip_finalize": (_c.c_int, [_c.c_void_p]),
     "bark_hip_encode_sub": (_c.c_int, [_c.c_void_p, _c.c_void_p, _c.c_int32, _c.c_int32, _c.c_void_p, _c.c_void_p]),
     "bark_hip_encode_mel": (
@@ -248,6 +249,32 @@ TDT_SHAPES = {
     "decoder.decoder_projector.weight": (640, 640), "decoder.decoder_projector.bias": (640,),
     "joint.head.weight": (8198, 640), "joint.head.bias": (8198,),
 }
+
+
+def probe(path) -> dict:
+    """What a safetensors checkpoint holds, from its header(s) alone
+    (weights_io::probe, src/weights_io.rs:208-297); needs no GPU."""
+    import json
+
+    buf = ctypes.create_string_buffer(4096)
+    _check(lib().bark_hip_probe(str(path).encode(), buf, len(buf)))
+    return json.loads(buf.value.decode())
+
+
+# The architecture this build runs (src/lib.rs cfg: LAYERS, HIDDEN, FFN, VOCAB).
+ARCH = {"layers": 24, "hidden": 1024, "ffn": 4096, "vocab": 8193}
+
+
+def check_architecture(info: dict) -> None:
+    """ModelInfo::check_architecture (src/weights_io.rs:173-195): refuse a
+    checkpoint whose shape differs from the compiled-in constants, naming both."""
+    got = tuple(info[k] for k in ("layers", "hidden", "ffn", "vocab"))
+    want = tuple(ARCH[k] for k in ("layers", "hidden", "ffn", "vocab"))
+    if got != want:
+        raise HipError(
+            f"this checkpoint is {got[0]}x{got[1]} (ffn {got[2]}, vocab {got[3]}), but this build is compiled for "
+            f"{want[0]}x{want[1]} (ffn {want[2]}, vocab {want[3]}): it is a different Parakeet variant, not a Bark 3.0 "
+            "release")
 
 
 class HipEncoder:

@@ -1326,6 +1326,15 @@ int bark_hip_load_safetensors(BarkHip* h, const char* path) {
   });
 }
 
+int bark_hip_probe(const char* path, char* buf, size_t cap) {
+  return guarded([&] {
+    BARK_REQUIRE(path && buf && cap > 0, "null argument");
+    const std::string r = safetensors_probe(path);
+    BARK_REQUIRE(r.size() < cap, "buffer too small for the probe result");
+    std::memcpy(buf, r.c_str(), r.size() + 1);
+  });
+}
+
 int bark_hip_finalize(BarkHip* h) {
   return guarded([&] {
     BARK_REQUIRE(h, "null handle");

@@ -260,6 +260,86 @@ std::vector<StTensor> safetensors_header(const std::string& file) {
   return out;
 }
 
+// probe (src/weights_io.rs:208-297): what a checkpoint holds, from its
+// header(s) alone, as a JSON object {release, layout, tensors, weights,
+// layers, hidden, ffn, vocab}. A 4-bit code word (U32) counts as eight
+// weights; per-row level tables (".levels") are not weights.
+std::string safetensors_probe(const std::string& path) {
+  const std::string dir = is_dir(path) ? path : "";
+  std::map<std::string, StTensor> entries;
+  for (const std::string& f : safetensors_files(path))
+    for (StTensor& t : safetensors_header(f)) entries[t.name] = std::move(t);
+  bool lowbit = false;
+  std::set<std::string> dtypes;
+  uint64_t weights = 0;
+  for (const auto& kv : entries) {
+    const std::string& name = kv.first;
+    if (name.size() >= 7 && name.compare(name.size() - 7, 7, ".levels") == 0) continue;
+    const std::string& dt = kv.second.dtype;
+    if (dt != "BF16" && dt != "F16" && dt != "F32" && dt != "U32") continue;  // never read
+    dtypes.insert(dt);
+    uint64_t n = 1;
+    for (int64_t d : kv.second.shape) n *= (uint64_t)d;
+    if (dt == "U32") {
+      lowbit = true;
+      n *= 8;
+    }
+    weights += n;
+  }
+  const bool lowbit_json = !dir.empty() && exists(dir + "/lowbit.json");
+  BARK_REQUIRE(!dtypes.count("U32") || lowbit_json || dir.empty(),
+               path + ": weights are stored as 4-bit codes but lowbit.json is missing");
+  lowbit = lowbit || lowbit_json;
+  const char* layout = lowbit ? "low-bit" : dtypes.count("BF16") ? "bf16" : dtypes.count("F16") ? "f16"
+                                                                            : dtypes.count("F32") ? "f32"
+                                                                                                  : nullptr;
+  BARK_REQUIRE(layout, path + ": no float or code tensors found");
+  auto ffn_w = entries.find("encoder.layers.0.feed_forward1.linear1.weight");
+  BARK_REQUIRE(ffn_w != entries.end() && ffn_w->second.shape.size() >= 2,
+               path + ": not a Parakeet TDT checkpoint (no feed_forward1)");
+  const int64_t ffn = ffn_w->second.shape[0];
+  const int64_t hidden = lowbit ? ffn_w->second.shape[1] * 8 : ffn_w->second.shape[1];
+  auto emb = entries.find("decoder.embedding.weight");
+  const int64_t vocab = emb != entries.end() && !emb->second.shape.empty() ? emb->second.shape[0] : 0;
+  std::set<long> layers;
+  const std::string pre = "encoder.layers.";
+  for (const auto& kv : entries) {
+    if (kv.first.compare(0, pre.size(), pre) != 0) continue;
+    const size_t dot = kv.first.find('.', pre.size());
+    if (dot == std::string::npos || dot == pre.size()) continue;
+    const std::string n = kv.first.substr(pre.size(), dot - pre.size());
+    if (n.find_first_not_of("0123456789") == std::string::npos && n.size() < 10) layers.insert(std::stol(n));
+  }
+  std::string release = "null";
+  if (!dir.empty() && exists(dir + "/bark3.json")) {
+    try {
+      const Json v = parse_json(read_text(dir + "/bark3.json"), dir + "/bark3.json");
+      const Json* src = v.get("source");
+      if (src && src->kind == Json::STR) {
+        release = "\"";
+        for (char ch : src->str) {  // JSON string escape
+          if (ch == '"' || ch == '\\') release += '\\', release += ch;
+          else if ((unsigned char)ch < 0x20) {
+            char b[8];
+            snprintf(b, sizeof b, "\\u%04x", ch);
+            release += b;
+          } else release += ch;
+        }
+        release += "\"";
+      }
+    } catch (const Error&) {
+      // an unreadable bark3.json names no release, as in the reference
+    }
+  }
+  char buf[384];
+  snprintf(buf, sizeof buf,
+           ",\"layout\":\"%s\",\"tensors\":%zu,\"weights\":%llu,\"layers\":%zu,\"hidden\":%lld,"
+           "\"ffn\":%lld,\"vocab\":%lld}",
+           layout, entries.size(), (unsigned long long)weights, layers.size(), (long long)hidden, (long long)ffn,
+           (long long)vocab);
+  return "{\"release\":" + release + buf;
+}
+
 void safetensors_read(const std::string& file, const StTensor& t, void* dst) {
   FILE* f = std::fopen(file.c_str(), "rb");
   BARK_REQUIRE(f, "cannot open " + file);

@@ -216,5 +216,8 @@ struct StTensor {
 std::vector<std::string> safetensors_files(const std::string& path);
 std::vector<StTensor> safetensors_header(const std::string& file);
 void safetensors_read(const std::string& file, const StTensor& t, void* dst);
+// what a checkpoint holds, from its header(s): JSON {release, layout, tensors,
+// weights, layers, hidden, ffn, vocab}
+std::string safetensors_probe(const std::string& path);
 
 }  // namespace bark

@@ -83,6 +83,12 @@ int bark_hip_set_lut4(BarkHip *h, const char *name, const uint8_t *codes,
  * then rounded to f16 as with bark_hip_set_f32); integer entries are skipped.
  * Tensors are read one at a time. Call before bark_hip_finalize. */
 int bark_hip_load_safetensors(BarkHip *h, const char *path);
+/* probe (src/weights_io.rs:208-297): what a safetensors checkpoint holds,
+ * from its header(s) alone, as JSON {"release": string|null, "layout":
+ * "bf16"|"f16"|"f32"|"low-bit", "tensors", "weights", "layers", "hidden",
+ * "ffn", "vocab"} (4-bit code words count eight weights; ".levels" tables are
+ * not weights) written to buf (cap bytes). Needs no device. */
+int bark_hip_probe(const char *path, char *buf, size_t cap);
 /* Fuses q|k|v (load_qkv, src/encoder.rs:342-402), folds BatchNorm
  * (src/encoder.rs:546-557), interleaves pw1 rows for the GLU epilogue and
  * uploads everything. Returns BARK_HIP_EINVAL naming a missing tensor. */
