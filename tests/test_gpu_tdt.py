@@ -217,3 +217,29 @@ def test_transcribe_vs_cpu_oracles(pkg, synth):
     assert margins.min() > 2e-3, f"oracle decision margin {margins.min():.2e} too small for this check"
     assert len(want) > 0
     np.testing.assert_array_equal(got, want)
+
+
+def test_tdt_error_paths(pkg, synth):
+    """no decoder tensors, no mel filters, bad lengths: clear errors, no decode"""
+    print("case tdt errors", flush=True)
+    enc = pkg.HipEncoder.load_with(synth.SynthCheckpoint(seed=1, n_layers=1), 0, 1)
+    try:
+        with pytest.raises(pkg.HipError, match="no TDT decoder tensors"):
+            enc.tdt_decode(synth.pooler(5, 0))
+    finally:
+        enc.close()
+    enc = make(pkg, synth, seed=0)
+    try:
+        with pytest.raises(pkg.HipError, match="set_mel_filters"):
+            enc.transcribe_wave_batch([np.zeros(1600, np.float32)])
+        import ctypes
+
+        out = np.zeros((4, 3), np.uint32)
+        n = ctypes.c_int32()
+        p = np.ascontiguousarray(synth.pooler(2, 0))
+        assert pkg.lib().bark_hip_tdt_decode(enc._h, p.ctypes.data, -1, out.ctypes.data, 4, ctypes.byref(n)) != 0
+        assert b"t_len out of range" in pkg.lib().bark_hip_last_error()
+        # the handle still decodes after the errors
+        np.testing.assert_array_equal(enc.tdt_decode(synth.pooler(7, 3)), oracle(synth, {"seed": 0}, 7, 3))
+    finally:
+        enc.close()
