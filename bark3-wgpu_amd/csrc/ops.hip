@@ -10,7 +10,22 @@ namespace {
 // load is a coalesced float4. mean = E[x], var = E[x^2] - mean^2 and
 // y = (x - mean) * (1/sqrt(var + 1e-5)) * w + b, the reference formula
 // (src/encoder/shader_sources.rs:185-228, src/cpu/ops.rs:15-56).
-__device__ inline void ln_row(float (&x)[16], const float* w, const float* b, int lane) {
+// w and b of a lane's 16 columns, loaded before the row statistics need them
+struct LnParams {
+  float w[16], b[16];
+  __device__ LnParams(const float* wp, const float* bp, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 4 * lane + 256 * i;
+      const floatx4 wv = *reinterpret_cast<const floatx4*>(wp + c);
+      const floatx4 bv = *reinterpret_cast<const floatx4*>(bp + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[4 * i + e] = wv[e], b[4 * i + e] = bv[e];
+    }
+  }
+};
+
+__device__ inline void ln_row(float (&x)[16], const LnParams& prm) {
   float s = 0.0f, q = 0.0f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -23,13 +38,7 @@ __device__ inline void ln_row(float (&x)[16], const float* w, const float* b, in
   const float var = q * (1.0f / 1024.0f) - mean * mean;
   const float inv = 1.0f / sqrtf(var + 1e-5f);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = 4 * lane + 256 * i;
-    const floatx4 wv = *reinterpret_cast<const floatx4*>(w + c);
-    const floatx4 bv = *reinterpret_cast<const floatx4*>(b + c);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) x[4 * i + e] = (x[4 * i + e] - mean) * inv * wv[e] + bv[e];
-  }
+  for (int i = 0; i < 16; ++i) x[i] = (x[i] - mean) * inv * prm.w[i] + prm.b[i];
 }
 
 __device__ inline void load_row(const float* x, float (&v)[16], int lane) {
@@ -57,8 +66,29 @@ __device__ inline void store_row16(half* y, const float (&v)[16], int lane) {
   }
 }
 
-// x += scale * (p_0 + p_1 + ...), partial sums added in split order.
+// x += scale * (p_0 + p_1 + ...), partial sums added in split order. Up to
+// four splits have all their loads issued before the first add.
+template <int S>
+__device__ inline void add_residual_n(float (&v)[16], const ResidIn& res, size_t row_off, int lane) {
+  float p[S][16];
+#pragma unroll
+  for (int s = 0; s < S; ++s) load_row(res.part + s * res.stride + row_off, p[s], lane);
+#pragma unroll
+  for (int s = 1; s < S; ++s)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[0][i] += p[s][i];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = v[i] + res.scale * p[0][i];
+}
+
 __device__ inline void add_residual(float (&v)[16], const ResidIn& res, size_t row_off, int lane) {
+  switch (res.splits) {
+    case 1: add_residual_n<1>(v, res, row_off, lane); return;
+    case 2: add_residual_n<2>(v, res, row_off, lane); return;
+    case 3: add_residual_n<3>(v, res, row_off, lane); return;
+    case 4: add_residual_n<4>(v, res, row_off, lane); return;
+    default: break;
+  }
   float p[16];
   load_row(res.part + row_off, p, lane);
   for (int s = 1; s < res.splits; ++s) {
@@ -76,13 +106,14 @@ __global__ void __launch_bounds__(256) ln_kernel(float* x, const float* w, const
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
+  const LnParams prm(w, b, lane);
   float v[16];
   load_row(x + (size_t)r * HIDDEN, v, lane);
   if (res.splits) {
     add_residual(v, res, (size_t)r * HIDDEN, lane);
     store_row32(x + (size_t)r * HIDDEN, v, lane);
   }
-  ln_row(v, w, b, lane);
+  ln_row(v, prm);
   if (y32) store_row32(y32 + (size_t)r * HIDDEN, v, lane);
   if (y16) store_row16(y16 + (size_t)r * HIDDEN, v, lane);
 }
@@ -105,12 +136,13 @@ __global__ void __launch_bounds__(256) ln2_kernel(const float* x, const float* w
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
+  const LnParams pa(wa, ba, lane), pb(wb, bb, lane);
   float v[16];
   load_row(x + (size_t)r * HIDDEN, v, lane);
   if (res.splits) add_residual(v, res, (size_t)r * HIDDEN, lane);
-  ln_row(v, wa, ba, lane);
+  ln_row(v, pa);
   store_row32(y32 + (size_t)r * HIDDEN, v, lane);
-  ln_row(v, wb, bb, lane);
+  ln_row(v, pb);
   store_row16(y16 + (size_t)r * HIDDEN, v, lane);
 }
 
