@@ -390,6 +390,31 @@ __global__ void __launch_bounds__(NT) rel_attn_kernel(AttnArgs a) {
 // has 16 workgroups per (query tile, head) and each thread streams one float4
 // per slot.
 constexpr int MERGE_Q = 8;
+// Combine S slots with every load issued before the first combine (the
+// running max and the sums keep slot order).
+template <int S>
+__device__ inline void merge_slots(const float* part_o, const float* part_ml, size_t sh0, size_t sstride, int d,
+                                   floatx4& o, float& l) {
+  float2 ml[S];
+  floatx4 v[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const size_t sh = sh0 + s * sstride;
+    ml[s] = *reinterpret_cast<const float2*>(part_ml + sh * 2);
+    v[s] = *reinterpret_cast<const floatx4*>(part_o + sh * HDIM + d);
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < S; ++s) m = fmaxf(m, ml[s].x);
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const float w = __builtin_amdgcn_exp2f(ml[s].x - m);
+    l += w * ml[s].y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] += w * v[s][e];
+  }
+}
+
 __global__ void __launch_bounds__(256) attn_merge_kernel(const float* part_o, const float* part_ml,
                                                          const int4* merges, half* out) {
   const int h = blockIdx.x % HEADS;
@@ -398,17 +423,25 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const float* part_o, co
   const int q = (rest % (BQ / MERGE_Q)) * MERGE_Q + (threadIdx.x >> 5);
   const int d = (threadIdx.x & 31) * 4;
   if (q >= mg.w) return;
-  float m = -INFINITY;
-  for (int s = 0; s < mg.y; ++s) m = fmaxf(m, part_ml[(((size_t)(mg.x + s) * HEADS + h) * BQ + q) * 2]);
   floatx4 o = {0.0f, 0.0f, 0.0f, 0.0f};
   float l = 0.0f;
-  for (int s = 0; s < mg.y; ++s) {
-    const size_t sh = ((size_t)(mg.x + s) * HEADS + h) * BQ + q;
-    const float w = __builtin_amdgcn_exp2f(part_ml[sh * 2] - m);
-    l += w * part_ml[sh * 2 + 1];
-    const floatx4 v = *reinterpret_cast<const floatx4*>(part_o + sh * HDIM + d);
+  const size_t sh0 = ((size_t)mg.x * HEADS + h) * BQ + q, sstride = (size_t)HEADS * BQ;
+  switch (mg.y) {
+    case 2: merge_slots<2>(part_o, part_ml, sh0, sstride, d, o, l); break;
+    case 3: merge_slots<3>(part_o, part_ml, sh0, sstride, d, o, l); break;
+    case 4: merge_slots<4>(part_o, part_ml, sh0, sstride, d, o, l); break;
+    default: {
+      float m = -INFINITY;
+      for (int s = 0; s < mg.y; ++s) m = fmaxf(m, part_ml[(sh0 + s * sstride) * 2]);
+      for (int s = 0; s < mg.y; ++s) {
+        const size_t sh = sh0 + s * sstride;
+        const float w = __builtin_amdgcn_exp2f(part_ml[sh * 2] - m);
+        l += w * part_ml[sh * 2 + 1];
+        const floatx4 v = *reinterpret_cast<const floatx4*>(part_o + sh * HDIM + d);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] += w * v[e];
+        for (int e = 0; e < 4; ++e) o[e] += w * v[e];
+      }
+    }
   }
   const float inv = 1.0f / l;
   const half4 w4 = {(half)(o[0] * inv), (half)(o[1] * inv), (half)(o[2] * inv), (half)(o[3] * inv)};
