@@ -897,7 +897,9 @@ int pick_wide_fm(int M, int N, int K, int splits = 1) {
   }();
   if (forced == 0 || (forced >= 2 && forced <= 6) || forced == 8) return forced;
   constexpr int CUS = 256;
-  if (K / splits <= 256) return 2;  // a few k-tiles: the prologue dominates
+  // a few k-tiles: the prologue dominates (measured: 3 blocks for the K = 256
+  // front-end pointwise GEMMs, 2 for split-K chunks of 256)
+  if (K / splits <= 256) return splits == 1 ? 3 : 2;
   int best = 2;
   double best_score = -1.0;
   const int fms[6] = {2, 3, 4, 5, 6, 8};
