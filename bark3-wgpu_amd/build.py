@@ -1,9 +1,13 @@
-"""Build recipe for libbark_hip.so (gfx950) — run by __graft_entry__.build().
+"""Build recipe for libbark_hip.so and libbark_hip.a (gfx950) — run by
+__graft_entry__.build().
 
-Each csrc/*.hip is compiled separately (in parallel) with hipcc for gfx950 and
-linked into bark3-wgpu_amd/libbark_hip.so, which the Python host layer loads
-with ctypes. Packed-FP32 instructions are disabled for device code
-(-packed-fp32-ops); hipcc's host pass prints a harmless warning about it.
+Each csrc/*.hip is compiled separately (in parallel) with hipcc for gfx950.
+The objects are linked into bark3-wgpu_amd/libbark_hip.so, which the Python
+host layer loads with ctypes, and archived into bark3-wgpu_amd/libbark_hip.a,
+the static library a Rust build.rs links (with amdhip64 and the C++ runtime:
+`-lamdhip64 -lstdc++`; each object carries its own gfx950 code object, so no
+device link step is needed). Packed-FP32 instructions are disabled for device
+code (-packed-fp32-ops); hipcc's host pass prints a harmless warning about it.
 """
 from __future__ import annotations
 
@@ -17,6 +21,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libbark_hip.so"
+STATIC = PKG / "libbark_hip.a"
 ARCH = os.environ.get("BARK_HIP_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -59,8 +64,15 @@ def build(verbose: bool = True) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}{r.stderr}")
     os.replace(tmp, LIB)
+    tmp_a = STATIC.with_suffix(".a.tmp")
+    if tmp_a.exists():
+        tmp_a.unlink()
+    r = subprocess.run(["ar", "rcs", str(tmp_a), *map(str, objs)], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"ar failed:\n{r.stdout}{r.stderr}")
+    os.replace(tmp_a, STATIC)
     if verbose:
-        print(f"built {LIB} from {len(sources)} sources")
+        print(f"built {LIB} and {STATIC.name} from {len(sources)} sources")
     return LIB
 
 

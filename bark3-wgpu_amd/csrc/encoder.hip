@@ -58,11 +58,6 @@ struct HostTensor {
   std::vector<uint8_t> codes;  // rows x cols/2
   std::vector<uint16_t> lut;   // rows x 16
   int64_t rows = 0, cols = 0;
-  int64_t numel() const {
-    int64_t n = 1;
-    for (auto s : shape) n *= s;
-    return n;
-  }
 };
 
 // A linear weight on the host side of finalize: f16 bits or codes + tables.
@@ -201,6 +196,39 @@ struct BarkHip {
   int n_layers = 24;
   hipStream_t stream = nullptr;
   std::mutex mu;
+  // Cross-stream ordering of calls on this handle: every call that queues
+  // work records `done` on its stream when it has queued everything, and the
+  // next call's stream waits for it first. The workspace buffers are shared
+  // by all calls, so a call on another stream must not start before the
+  // previous one has finished with them.
+  hipEvent_t done = nullptr;
+  hipStream_t done_stream = nullptr;
+  void order_after_previous(hipStream_t st) {
+    if (done_stream && done_stream != st) BARK_HIP_CHECK(hipStreamWaitEvent(st, done, 0));
+  }
+  void mark_done(hipStream_t st) {
+    BARK_HIP_CHECK(hipEventRecord(done, st));
+    done_stream = st;
+  }
+  // runs f (which queues work on st) ordered after the previous call
+  template <class F>
+  void on_stream(hipStream_t st, F&& f) {
+    order_after_previous(st);
+    try {
+      f();
+    } catch (...) {
+      (void)hipEventRecord(done, st);  // whatever was queued before the error
+      done_stream = st;
+      throw;
+    }
+    mark_done(st);
+  }
+  // pinned staging of the plan tables (bounds, attention segments, merges,
+  // lanes): host memory that lives until the copies reading it have run
+  // (tables_copied), so a new packing needs no stream synchronisation
+  void* tables_host = nullptr;
+  size_t tables_host_cap = 0;
+  hipEvent_t tables_copied = nullptr;
   std::map<std::string, HostTensor> staged;
   bool finalized = false;
   bool has_front_end = false;
@@ -328,6 +356,9 @@ struct BarkHip {
     for (DevBuf* b : bufs)
       if (b->p) (void)hipFree(b->p);
     if (stream) (void)hipStreamDestroy(stream);
+    if (done) (void)hipEventDestroy(done);
+    if (tables_copied) (void)hipEventDestroy(tables_copied);
+    if (tables_host) (void)hipHostFree(tables_host);
   }
 
   // ------------------------------------------------------------ finalize --
@@ -787,20 +818,35 @@ struct BarkHip {
     std::vector<int4> tl, ml;
     std::vector<int> ll;
     attention_tables(pl, tl, ll, ml);
-    BARK_HIP_CHECK(hipMemcpyAsync(bounds.p, b.data(), b.size() * sizeof(int2),
-                                  hipMemcpyHostToDevice, st));
-    BARK_HIP_CHECK(hipMemcpyAsync(tiles.p, tl.data(), tl.size() * sizeof(int4),
-                                  hipMemcpyHostToDevice, st));
-    if (!ml.empty())
-      BARK_HIP_CHECK(hipMemcpyAsync(merges.p, ml.data(), ml.size() * sizeof(int4),
-                                    hipMemcpyHostToDevice, st));
-    BARK_HIP_CHECK(hipMemcpyAsync(attn_lanes.p, ll.data(), ll.size() * sizeof(int), hipMemcpyHostToDevice, st));
+    // the four tables back to back in pinned host memory; the previous
+    // tables' copies must have read theirs before it is overwritten (they
+    // normally finished long ago: this wait is not a stream synchronisation)
+    const size_t nb = b.size() * sizeof(int2), nt = tl.size() * sizeof(int4), nm = ml.size() * sizeof(int4),
+                 nl = ll.size() * sizeof(int);
+    const size_t total = nb + nt + nm + nl;
+    BARK_HIP_CHECK(hipEventSynchronize(tables_copied));
+    if (total > tables_host_cap) {
+      if (tables_host) BARK_HIP_CHECK(hipHostFree(tables_host));
+      tables_host = nullptr;
+      tables_host_cap = 0;
+      BARK_HIP_CHECK(hipHostMalloc(&tables_host, total, hipHostMallocDefault));
+      tables_host_cap = total;
+    }
+    char* hp = static_cast<char*>(tables_host);
+    std::memcpy(hp, b.data(), nb);
+    std::memcpy(hp + nb, tl.data(), nt);
+    if (nm) std::memcpy(hp + nb + nt, ml.data(), nm);
+    std::memcpy(hp + nb + nt + nm, ll.data(), nl);
+    BARK_HIP_CHECK(hipMemcpyAsync(bounds.p, hp, nb, hipMemcpyHostToDevice, st));
+    BARK_HIP_CHECK(hipMemcpyAsync(tiles.p, hp + nb, nt, hipMemcpyHostToDevice, st));
+    if (nm) BARK_HIP_CHECK(hipMemcpyAsync(merges.p, hp + nb + nt, nm, hipMemcpyHostToDevice, st));
+    BARK_HIP_CHECK(hipMemcpyAsync(attn_lanes.p, hp + nb + nt + nm, nl, hipMemcpyHostToDevice, st));
+    BARK_HIP_CHECK(hipEventRecord(tables_copied, st));
     ntiles = (int)tl.size();
     nlanes = (int)ll.size() - 1;
     nmerges = (int)ml.size();
     nparts = 0;
     for (const auto& m : ml) nparts += m.y;
-    BARK_HIP_CHECK(hipStreamSynchronize(st));  // host vectors go out of scope
     table_key = key;
   }
   int ntiles = 0, nlanes = 0, nmerges = 0, nparts = 0;
@@ -1181,9 +1227,11 @@ int bark_hip_create(int device, int n_layers, BarkHip** out) {
     h->device = device;
     h->n_layers = n_layers;
     hipError_t e = hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&h->done, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&h->tables_copied, hipEventDisableTiming);
     if (e != hipSuccess) {
       delete h;
-      throw Error{std::string("hipStreamCreate: ") + hipGetErrorString(e)};
+      throw Error{std::string("hipStreamCreate/hipEventCreate: ") + hipGetErrorString(e)};
     }
     *out = h;
   });
@@ -1204,7 +1252,8 @@ int bark_hip_set_f32(BarkHip* h, const char* name, const float* v, const int64_t
     t = HostTensor();
     t.kind = HostTensor::F32;
     t.shape.assign(shape, shape + ndim);
-    const int64_t n = t.numel();
+    for (int64_t d : t.shape) BARK_REQUIRE(d >= 0, "negative dimension");
+    const int64_t n = shape_elements(t.shape, name ? name : "tensor");
     BARK_REQUIRE(n > 0, "empty tensor");
     t.f32.assign(v, v + n);
   });
@@ -1289,8 +1338,7 @@ int bark_hip_load_safetensors(BarkHip* h, const char* path) {
     for (const std::string& file : safetensors_files(path)) {
       for (const StTensor& t : safetensors_header(file)) {
         if (!wanted(t.name)) continue;
-        int64_t n = 1;
-        for (int64_t d : t.shape) n *= d;
+        const int64_t n = t.numel;  // overflow-checked by the header reader
         const uint64_t bytes = t.end - t.begin;
         HostTensor v;
         v.shape = t.shape;
@@ -1350,7 +1398,7 @@ int bark_hip_encode_sub(BarkHip* h, const float* sub_rows, int32_t t, int32_t du
     BARK_REQUIRE(h && sub_rows, "null argument");
     std::lock_guard<std::mutex> lk(h->mu);
     BARK_HIP_CHECK(hipSetDevice(h->device));
-    h->encode_sub(sub_rows, t, dump_layer, pooler, block);
+    h->on_stream(h->stream, [&] { h->encode_sub(sub_rows, t, dump_layer, pooler, block); });
   });
 }
 
@@ -1360,8 +1408,9 @@ int bark_hip_encode_mel(BarkHip* h, const float* mel, int32_t n_frames, int32_t 
     BARK_REQUIRE(h && mel && pooler, "null argument");
     std::lock_guard<std::mutex> lk(h->mu);
     BARK_HIP_CHECK(hipSetDevice(h->device));
-    h->encode_mel_batch(mel, false, &n_frames, &n_valid, 1, t_out, pooler, false, pooler_cap,
-                        h->stream);
+    h->on_stream(h->stream, [&] {
+      h->encode_mel_batch(mel, false, &n_frames, &n_valid, 1, t_out, pooler, false, pooler_cap, h->stream);
+    });
   });
 }
 
@@ -1372,8 +1421,9 @@ int bark_hip_encode_mel_batch(BarkHip* h, const float* mel, const int32_t* n_fra
     BARK_REQUIRE(h && mel && pooler, "null argument");
     std::lock_guard<std::mutex> lk(h->mu);
     BARK_HIP_CHECK(hipSetDevice(h->device));
-    h->encode_mel_batch(mel, false, n_frames, n_valid, batch, t_out, pooler, false, pooler_cap,
-                        h->stream);
+    h->on_stream(h->stream, [&] {
+      h->encode_mel_batch(mel, false, n_frames, n_valid, batch, t_out, pooler, false, pooler_cap, h->stream);
+    });
   });
 }
 
@@ -1385,8 +1435,9 @@ int bark_hip_encode_mel_batch_device(BarkHip* h, const float* d_mel, const int32
     std::lock_guard<std::mutex> lk(h->mu);
     BARK_HIP_CHECK(hipSetDevice(h->device));
     hipStream_t st = stream ? static_cast<hipStream_t>(stream) : h->stream;
-    h->encode_mel_batch(d_mel, true, n_frames, n_valid, batch, t_out, d_pooler, true,
-                        pooler_cap, st);
+    h->on_stream(st, [&] {
+      h->encode_mel_batch(d_mel, true, n_frames, n_valid, batch, t_out, d_pooler, true, pooler_cap, st);
+    });
   });
 }
 
@@ -1410,11 +1461,13 @@ int bark_hip_mel(BarkHip* h, const float* wave, int64_t n_samples, float* featur
     BARK_REQUIRE(cap >= nf * MEL, "features buffer too small");
     h->ensure(h->mel_wave, (size_t)n_samples * 4);
     h->ensure(h->mel_feat, nf * MEL * 4);
-    BARK_HIP_CHECK(hipMemcpyAsync(h->mel_wave.p, wave, (size_t)n_samples * 4, hipMemcpyHostToDevice, h->stream));
-    h->run_mel(h->mel_wave.as<float>(), (long)n_samples, h->mel_feat.as<float>(), nf * MEL, n_frames, n_valid,
-               h->stream);
-    BARK_HIP_CHECK(hipMemcpyAsync(features, h->mel_feat.p, nf * MEL * 4, hipMemcpyDeviceToHost, h->stream));
-    BARK_HIP_CHECK(hipStreamSynchronize(h->stream));
+    h->on_stream(h->stream, [&] {
+      BARK_HIP_CHECK(hipMemcpyAsync(h->mel_wave.p, wave, (size_t)n_samples * 4, hipMemcpyHostToDevice, h->stream));
+      h->run_mel(h->mel_wave.as<float>(), (long)n_samples, h->mel_feat.as<float>(), nf * MEL, n_frames, n_valid,
+                 h->stream);
+      BARK_HIP_CHECK(hipMemcpyAsync(features, h->mel_feat.p, nf * MEL * 4, hipMemcpyDeviceToHost, h->stream));
+      BARK_HIP_CHECK(hipStreamSynchronize(h->stream));
+    });
   });
 }
 
@@ -1425,7 +1478,7 @@ int bark_hip_mel_device(BarkHip* h, const float* d_wave, int64_t n_samples, floa
     std::lock_guard<std::mutex> lk(h->mu);
     BARK_HIP_CHECK(hipSetDevice(h->device));
     hipStream_t st = stream ? static_cast<hipStream_t>(stream) : h->stream;
-    h->run_mel(d_wave, (long)n_samples, d_features, cap, n_frames, n_valid, st);
+    h->on_stream(st, [&] { h->run_mel(d_wave, (long)n_samples, d_features, cap, n_frames, n_valid, st); });
   });
 }
 
@@ -1435,7 +1488,7 @@ int bark_hip_encode_wave_batch(BarkHip* h, const float* waves, const int64_t* n_
     BARK_REQUIRE(h && waves && n_samples && pooler, "null argument");
     std::lock_guard<std::mutex> lk(h->mu);
     BARK_HIP_CHECK(hipSetDevice(h->device));
-    h->encode_wave_batch(waves, n_samples, batch, t_out, pooler, pooler_cap);
+    h->on_stream(h->stream, [&] { h->encode_wave_batch(waves, n_samples, batch, t_out, pooler, pooler_cap); });
   });
 }
 
@@ -1464,11 +1517,12 @@ int bark_hip_tdt_decode_batch(BarkHip* h, const float* pooler, const int32_t* t_
       BARK_REQUIRE(total < (1u << 31), "too many frames");
     }
     BARK_REQUIRE(pooler || total == 0, "null pooler");
-    if (total > 0) {
-      h->ensure(h->tdt_pooler, total * 640 * 4);
-      BARK_HIP_CHECK(hipMemcpyAsync(h->tdt_pooler.p, pooler, total * 640 * 4, hipMemcpyHostToDevice, h->stream));
-    }
-    h->tdt_decode_copy(h->tdt_pooler.as<float>(), rows.data(), t_lens, batch, tokens, cap, n_tokens, h->stream);
+    if (total > 0) h->ensure(h->tdt_pooler, total * 640 * 4);
+    h->on_stream(h->stream, [&] {
+      if (total > 0)
+        BARK_HIP_CHECK(hipMemcpyAsync(h->tdt_pooler.p, pooler, total * 640 * 4, hipMemcpyHostToDevice, h->stream));
+      h->tdt_decode_copy(h->tdt_pooler.as<float>(), rows.data(), t_lens, batch, tokens, cap, n_tokens, h->stream);
+    });
   });
 }
 
@@ -1487,7 +1541,7 @@ int bark_hip_tdt_decode_batch_device(BarkHip* h, const float* d_pooler, const in
       total += (size_t)t_lens[u];
       BARK_REQUIRE(total < (1u << 31), "too many frames");
     }
-    h->tdt_decode_copy(d_pooler, rows.data(), t_lens, batch, tokens, cap, n_tokens, st);
+    h->on_stream(st, [&] { h->tdt_decode_copy(d_pooler, rows.data(), t_lens, batch, tokens, cap, n_tokens, st); });
   });
 }
 
@@ -1497,7 +1551,7 @@ int bark_hip_transcribe_wave_batch(BarkHip* h, const float* waves, const int64_t
     BARK_REQUIRE(h && waves && n_samples && n_tokens, "null argument");
     std::lock_guard<std::mutex> lk(h->mu);
     BARK_HIP_CHECK(hipSetDevice(h->device));
-    h->transcribe_wave_batch(waves, n_samples, batch, t_out, tokens, cap, n_tokens);
+    h->on_stream(h->stream, [&] { h->transcribe_wave_batch(waves, n_samples, batch, t_out, tokens, cap, n_tokens); });
   });
 }
 

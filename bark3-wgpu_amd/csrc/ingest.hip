@@ -190,12 +190,24 @@ std::string read_text(const std::string& path) {
   return out;
 }
 
+// A non-negative integer below 2^53 (every such integer is exact in the
+// double the parser holds; larger values are rejected before any cast).
 int64_t as_int(const Json& v, const std::string& where) {
-  BARK_REQUIRE(v.kind == Json::NUM && v.num >= 0 && v.num == (double)(int64_t)v.num, where + ": expected an integer");
+  BARK_REQUIRE(v.kind == Json::NUM && v.num >= 0 && v.num < 9007199254740992.0 &&
+                   v.num == (double)(int64_t)v.num,
+               where + ": expected an integer below 2^53");
   return (int64_t)v.num;
 }
 
 }  // namespace
+
+int64_t shape_elements(const std::vector<int64_t>& shape, const std::string& where) {
+  int64_t n = 1;
+  for (int64_t d : shape)
+    BARK_REQUIRE(!__builtin_mul_overflow(n, d, &n) && n < (int64_t(1) << 53),
+                 where + ": element count of the shape overflows");
+  return n;
+}
 
 std::vector<std::string> safetensors_files(const std::string& path) {
   if (!is_dir(path)) {
@@ -252,6 +264,7 @@ std::vector<StTensor> safetensors_header(const std::string& file) {
     t.name = kv.first;
     t.dtype = dt->str;
     for (const auto& d : sh->arr) t.shape.push_back(as_int(d, where));
+    t.numel = shape_elements(t.shape, where);
     t.begin = data + (uint64_t)as_int(off->arr[0], where);
     t.end = data + (uint64_t)as_int(off->arr[1], where);
     BARK_REQUIRE(t.begin <= t.end && t.end - data <= avail, where + ": data outside the file");
@@ -278,8 +291,7 @@ std::string safetensors_probe(const std::string& path) {
     const std::string& dt = kv.second.dtype;
     if (dt != "BF16" && dt != "F16" && dt != "F32" && dt != "U32") continue;  // never read
     dtypes.insert(dt);
-    uint64_t n = 1;
-    for (int64_t d : kv.second.shape) n *= (uint64_t)d;
+    uint64_t n = (uint64_t)kv.second.numel;
     if (dt == "U32") {
       lowbit = true;
       n *= 8;

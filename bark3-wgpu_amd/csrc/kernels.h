@@ -209,8 +209,11 @@ const int* tdt_current(const TdtDev& d, long launches, int u);
 struct StTensor {
   std::string name, dtype;
   std::vector<int64_t> shape;
+  int64_t numel = 0;  // product of shape, checked against overflow when parsed
   uint64_t begin = 0, end = 0;
 };
+// product of a shape's entries; throws when it overflows (or reaches 2^53)
+int64_t shape_elements(const std::vector<int64_t>& shape, const std::string& where);
 // the files of a checkpoint: a .safetensors file, or a directory holding
 // model.safetensors or model.safetensors.index.json and its shards
 std::vector<std::string> safetensors_files(const std::string& path);

@@ -16,7 +16,17 @@
  *    counterpart of the reference's `anyhow::Error`.
  *  - Host pointers are borrowed for the duration of the call only.
  *  - Calls on one handle are serialised by an internal mutex (the reference
- *    shares `&AsrInference` across threads, src/inference.rs:17-18).
+ *    shares `&AsrInference` across threads, src/inference.rs:17-18). The
+ *    mutex orders the host side; the device side is ordered too: every call
+ *    records an event on the stream it queued its work on, and a call on a
+ *    different stream waits for that event before its first kernel, because
+ *    all calls share the handle's workspace buffers. So device-form calls on
+ *    several streams are safe, but calls on one handle never overlap on the
+ *    device; use one handle per stream for concurrent encodes.
+ *  - A device-form call returns without synchronising with the device, also
+ *    when the batch packing changes (the plan tables are staged in pinned
+ *    host memory). It blocks only when a workspace buffer must grow (the old
+ *    buffer may still be in use), i.e. the first time a larger batch is seen.
  *  - No C++ exceptions cross this boundary.
  */
 #ifndef BARK_HIP_H
@@ -197,7 +207,13 @@ int bark_hip_profile_report(BarkHip *h, char *buf, size_t cap);
  * src/encoder.rs:1039-1100, in the generic table format): device pointers
  * A (T, K) activations, codes (N, K/2) bytes, lut16 (N, 16) f16, C (T, N).
  * a_dtype: 0 = f16, 1 = bf16. c_dtype: 0 = f32, 1 = f16, 2 = bf16.
- * K % 256 == 0, N % 128 == 0. Queued on `stream`, not synchronised. */
+ * K % 256 == 0, N % 128 == 0. Queued on `stream`, not synchronised.
+ * The product runs on f16 MFMA (the levels are f16, so dequantisation is
+ * exact; accumulation is f32). bf16 activations are converted to f16 on the
+ * way into the tile: exact for 0 and for 6.104e-5 <= |a| <= 65504 (every bf16
+ * value in the f16 normal range); smaller magnitudes are rounded to f16
+ * subnormals (absolute error <= 3e-8, below 3e-8 they become 0) and larger
+ * ones overflow to +-inf. */
 int bark_hip_lowbit_linear(const void *A, int32_t a_dtype, const uint8_t *codes,
                            const uint16_t *lut16, void *C, int32_t c_dtype, int32_t T,
                            int32_t K, int32_t N, void *stream);

@@ -55,10 +55,74 @@ def test_config3_lowbit_t2207(pkg, synth, oracle):
         orc = oracle.Encoder(src, 24)
         sub = oracle.subsample(src, mel)
         want_pool, want_dumps = orc.encode_dump(sub, t)
-        errs = [(l, rel_max_abs(enc.encode(sub, t, dump_layer=l).block, want_dumps[l])) for l in (0, 1, 11, 23)]
+        errs = [(l, rel_max_abs(enc.encode(sub, t, dump_layer=l).block, want_dumps[l])) for l in range(24)]
     e_pool = rel_max_abs(pooler, want_pool)
-    print("  per-layer rel max-abs:", " ".join(f"{l}:{e:.1e}" for l, e in errs), f" pooler {e_pool:.2e}")
+    print("  per-layer rel max-abs (pre-norm residual of each block vs the oracle):")
+    for l, e in errs:
+        print(f"    layer {l:2d}  {e:.2e}")
+    print(f"    pooler    {e_pool:.2e}")
     assert max(e for _, e in errs) <= TOL and e_pool <= TOL
+
+
+def test_config4_batch_16_utterances(pkg, synth, oracle):
+    """configs[4] at its real workload: 16 utterances of U(5, 60) s (seeded)
+    through the 24-block 4-bit encoder as one packed batch. Every utterance
+    equals its own batch-1 encode_mel bit for bit (the reference runs the
+    chunks one after another, src/inference.rs:311-326), and the shortest and
+    the longest match the oracle per layer."""
+    rng = np.random.default_rng(4)
+    secs = rng.uniform(5.0, 60.0, size=16)
+    frames = [int(s * 100) for s in secs]
+    ts = [pkg.conv_len(pkg.conv_len(pkg.conv_len(f))) for f in frames]
+    print(f"case config4 batch of 16: frames={frames} T={ts}", flush=True)
+    src = synth.SynthCheckpoint(seed=44, n_layers=24, style="rich", lowbit=True)
+    mels = [synth.mel(f, seed=100 + i) for i, f in enumerate(frames)]
+    with pkg.HipEncoder.load_with(src, n_layers=24) as enc:
+        batch = enc.encode_mel_batch(mels)
+        singles = [enc.encode_mel(m)[0] for m in mels]
+        for i, (b, s1) in enumerate(zip(batch, singles)):
+            assert b.shape == (ts[i], 640) and b.shape == s1.shape
+            assert np.array_equal(b, s1), f"utterance {i} (T={ts[i]}) differs from its own encode"
+        print("  16 of 16 batch results bit-identical to their batch-1 encodes", flush=True)
+        orc = oracle.Encoder(src, 24)
+        for i in (int(np.argmin(frames)), int(np.argmax(frames))):
+            sub = oracle.subsample(src, mels[i])
+            t = ts[i]
+            want_pool, want_dumps = orc.encode_dump(sub, t)
+            errs = [rel_max_abs(enc.encode(sub, t, dump_layer=l).block, want_dumps[l]) for l in range(24)]
+            e_pool = rel_max_abs(batch[i], want_pool)
+            print(f"  utterance {i} T={t}: per-layer max {max(errs):.2e} (layer {int(np.argmax(errs))}), "
+                  f"batched pooler {e_pool:.2e}", flush=True)
+            assert max(errs) <= TOL and e_pool <= TOL
+
+
+def test_two_streams_back_to_back(pkg, synth):
+    """Device-form calls on one handle from two streams, queued back to back
+    without a host synchronisation between them: the second call waits for the
+    first on the device (they share the handle's workspace), so both results
+    equal single-stream runs."""
+    import torch
+
+    src = synth.SynthCheckpoint(seed=45, n_layers=2, style="rich", lowbit=True)
+    fa, fb = 2400, 1300
+    ma, mb = synth.mel(fa, seed=1), synth.mel(fb, seed=2)
+    ta = pkg.conv_len(pkg.conv_len(pkg.conv_len(fa)))
+    tb = pkg.conv_len(pkg.conv_len(pkg.conv_len(fb)))
+    print(f"case two streams T={ta},{tb}", flush=True)
+    with pkg.HipEncoder.load_with(src, n_layers=2) as enc:
+        want_a, _ = enc.encode_mel(ma)
+        want_b, _ = enc.encode_mel(mb)
+        da, db = torch.from_numpy(ma).cuda(), torch.from_numpy(mb).cuda()
+        pa = torch.full((ta, 640), float("nan"), device="cuda")
+        pb = torch.full((tb, 640), float("nan"), device="cuda")
+        s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+        torch.cuda.synchronize()
+        for _ in range(3):
+            enc.encode_mel_batch_device(da.data_ptr(), [fa], [fa], pa.data_ptr(), pa.numel(), s1.cuda_stream)
+            enc.encode_mel_batch_device(db.data_ptr(), [fb], [fb], pb.data_ptr(), pb.numel(), s2.cuda_stream)
+        torch.cuda.synchronize()
+        got_a, got_b = pa.cpu().numpy(), pb.cpu().numpy()
+    assert np.array_equal(got_a, want_a) and np.array_equal(got_b, want_b)
 
 
 def test_batch_equals_individual(pkg, synth):

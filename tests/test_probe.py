@@ -120,6 +120,12 @@ def test_json_edge_cases(pkg, tmp_path):
     (b'{"a": {"dtype": "F32", "shape": [1.5], "data_offsets": [0, 4]}}', "expected an integer"),
     (b'{"a": {"dtype": "F32", "shape": [1]}}', "malformed tensor entry"),
     (b'{"a": 1} x', "trailing data"),
+    # 2^63 and above would be undefined in a cast to int64: rejected first
+    (b'{"a": {"dtype": "F32", "shape": [9223372036854775808], "data_offsets": [0, 4]}}', "below 2\\^53"),
+    (b'{"a": {"dtype": "F32", "shape": [1e300], "data_offsets": [0, 4]}}', "below 2\\^53"),
+    # each entry is fine, their product wraps a 64-bit count: rejected, not wrapped
+    (b'{"a": {"dtype": "F32", "shape": [4294967296, 4294967296, 16], "data_offsets": [0, 4]}}', "overflows"),
+    (b'{"a": {"dtype": "F32", "shape": [134217728, 134217728], "data_offsets": [0, 4]}}', "overflows"),
 ])
 def test_malformed_headers(pkg, tmp_path, raw, match):
     header_file(tmp_path / "model.safetensors", {}, raw_header=raw, pad=16)
