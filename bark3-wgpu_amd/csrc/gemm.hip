@@ -392,6 +392,146 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
   }
 }
 
+// Epilogue of a (32*FM) x 64 wave tile. Lane (l32, lhi) holds, for MFMA block (i, j), column
+// nw + 32j + l32 and rows m0 + 32i + 8g + 4lhi + b of acc[i][j][4g + b].
+// Column-dependent work (bias, head/dim split, output base) is done once
+// per column; row offsets are compile-time multiples of the row stride; a
+// tile inside M skips the per-row bound checks. bz selects the split-K slab.
+template <int FM, int EPI>
+__device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p, int m0, int nw, int bz, int lane,
+                                     int ib = 0, int ie = FM) {
+  const int l32 = lane & 31, lhi = lane >> 5;
+  EpiArgs ea = p.ea;
+  if constexpr (EPI == (int)Epi::StoreF32) ea.out_f32 += bz * p.out_zstride;
+  const int mrow = m0 + 4 * lhi;  // row of acc element v = 0 of block i = 0
+  auto epilogue = [&](auto checked) {
+  constexpr bool CHK = decltype(checked)::value;
+  auto row_ok = [&](int rl) { return !CHK || mrow + rl < p.M; };  // rl = 32i + 8g + b
+  if constexpr (EPI == (int)Epi::Glu) {
+    float* base = ea.out_f32 + (size_t)mrow * ea.ldo + (nw >> 1) + l32;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) if (i >= ib && i < ie)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
+        if (row_ok(rl)) base[(size_t)rl * ea.ldo] = fast_sigmoid_mul(acc[i][0][v], acc[i][1][v]);
+      }
+  } else if constexpr (EPI == (int)Epi::Qkv) {
+    const int region = __builtin_amdgcn_readfirstlane(nw >> 10);  // 0 q, 1 k, 2 v (wave-uniform)
+    if (region == 2) {
+      // V^T[h][d][r]: a lane's four consecutive rows are contiguous, one 8-byte store
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int hd = nw - 2048 + 32 * j + l32;  // h*128 + d
+        half* vrow = ea.vt + (size_t)hd * ea.mp + mrow;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) if (i >= ib && i < ie)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int rl = 32 * i + 8 * g;
+            if (!CHK || mrow + rl + 3 < p.M) {
+              const half4 w4 = {to_f16(acc[i][j][4 * g]), to_f16(acc[i][j][4 * g + 1]),
+                                to_f16(acc[i][j][4 * g + 2]), to_f16(acc[i][j][4 * g + 3])};
+              *reinterpret_cast<half4*>(vrow + rl) = w4;
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (mrow + rl + e < p.M) vrow[rl + e] = to_f16(acc[i][j][4 * g + e]);
+            }
+          }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int hd = (nw & 1023) + 32 * j + l32, h = hd >> 7, d = hd & 127;
+        const size_t off = ((size_t)h * ea.mp + mrow) * HDIM + d;
+        if (region == 0) {
+          const float bu = ea.bu[hd], bv = ea.bv[hd];
+          half* pu = ea.qu + off;
+          half* pv = ea.qv + off;
+#pragma unroll
+          for (int i = 0; i < FM; ++i) if (i >= ib && i < ie)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
+              if (row_ok(rl)) {
+                pu[rl * HDIM] = to_f16((acc[i][j][v] + bu) * ea.scale);
+                pv[rl * HDIM] = to_f16((acc[i][j][v] + bv) * ea.scale);
+              }
+            }
+        } else {
+          half* pk = ea.kh + off;
+#pragma unroll
+          for (int i = 0; i < FM; ++i) if (i >= ib && i < ie)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
+              if (row_ok(rl)) pk[rl * HDIM] = to_f16(acc[i][j][v]);
+            }
+        }
+      }
+    }
+  } else if constexpr (EPI == (int)Epi::RelK) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = nw + 32 * j + l32, h = c >> 7, d = c & 127;
+      half* pr = ea.rk + ((size_t)h * ea.pp + mrow) * HDIM + d;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) if (i >= ib && i < ie)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
+          if (row_ok(rl)) pr[rl * HDIM] = to_f16(acc[i][j][v]);
+        }
+    }
+  } else if constexpr (EPI == (int)Epi::StoreF16 || EPI == (int)Epi::StoreBF16 || EPI == (int)Epi::Silu ||
+                       EPI == (int)Epi::BiasReluF16) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = nw + 32 * j + l32;
+      const float bc = ea.bias ? ea.bias[c] : 0.0f;
+      const size_t base = (size_t)mrow * ea.ldo + c;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) if (i >= ib && i < ie)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
+          if (!row_ok(rl)) continue;
+          const size_t at = base + (size_t)rl * ea.ldo;
+          const float x = acc[i][j][v];
+          if constexpr (EPI == (int)Epi::StoreF16) {
+            ea.out_f16[at] = to_f16(x + bc);
+          } else if constexpr (EPI == (int)Epi::StoreBF16) {
+            uint32_t u = __float_as_uint(x + bc);
+            u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite inputs)
+            reinterpret_cast<uint16_t*>(ea.out_f16)[at] = (uint16_t)(u >> 16);
+          } else if constexpr (EPI == (int)Epi::Silu) {
+            ea.out_f16[at] = to_f16(fast_sigmoid_mul(x, x));
+          } else {
+            const float y = x + bc;
+            ea.out_f16[at] = to_f16(y > 0.0f ? y : 0.0f);
+          }
+        }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) if (i >= ib && i < ie)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = m0 + i * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
+          if (r < p.M) store_one<EPI>(ea, r, nw + 32 * j + l32, acc[i][j][v]);
+        }
+  }
+  };
+  // a tile inside M skips every per-row check (the f32 store, the split-K
+  // partial, measured faster with the checks kept: one code path)
+  if constexpr (EPI == (int)Epi::StoreF32 || EPI == (int)Epi::FlattenReluF16) epilogue(std::integral_constant<bool, true>());
+  else if (m0 + 32 * FM <= p.M) epilogue(std::integral_constant<bool, false>());
+  else epilogue(std::integral_constant<bool, true>());
+}
+
 // Wide-tile kernel: workgroup tile (32*FM) x 256, the four waves side by
 // side, each owning all rows and 64 columns (FM x 2 MFMA blocks). B never
 // touches LDS: an MFMA B fragment is 8 consecutive k of one weight row, i.e.
@@ -610,141 +750,487 @@ __global__ void __launch_bounds__(256, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kern
     __syncthreads();
   }
 
-  // Epilogue. Lane (l32, lhi) holds, for MFMA block (i, j), column
-  // nw + 32j + l32 and rows m0 + 32i + 8g + 4lhi + b of acc[i][j][4g + b].
-  // Column-dependent work (bias, head/dim split, output base) is done once
-  // per column; row offsets are compile-time multiples of the row stride; a
-  // tile inside M skips the per-row bound checks.
-  EpiArgs ea = p.ea;
-  if constexpr (EPI == (int)Epi::StoreF32) ea.out_f32 += bz * p.out_zstride;
-  const int mrow = m0 + 4 * lhi;  // row of acc element v = 0 of block i = 0
-  auto epilogue = [&](auto checked) {
-  constexpr bool CHK = decltype(checked)::value;
-  auto row_ok = [&](int rl) { return !CHK || mrow + rl < p.M; };  // rl = 32i + 8g + b
+  tile_epilogue<FM, EPI>(acc, p, m0, nw, bz, lane);
+}
+
+// Two-group tile kernel: 512 threads = two K-groups of four waves. Wave
+// (g, w) computes the same (32*FM) x 64 tile as wave w of gemm_wide_kernel;
+// of every 64-k tile, group g runs the 16-k slices 2g and 2g + 1 (k = 32h +
+// 8s .. +7 for lane half h, slice s, the wide kernel's permuted order). Waves
+// w and w + 4 share a SIMD, so every SIMD runs two waves of one tile and one
+// wave's code expansion (VALU) proceeds while the other's MFMAs do: within
+// one wave the two barely overlap, across two waves of a SIMD they do
+// (measured on MI355X). Launches with fewer tiles than CUs therefore still
+// run two waves per SIMD.
+//
+// Operands reach LDS by direct global->LDS loads (global_load_lds_dwordx4, 16
+// bytes per lane, no staging registers), issued NS - 1 k-tiles ahead into NS
+// stages shared by both groups:
+//  - A in unpadded 128-byte rows whose 16-byte chunks are XOR-swizzled by row
+//    pair (chunk c of row r at position c ^ ((r >> 1) & 7)): LDS serves 256
+//    bytes per clock, two 128-byte rows side by side, so the fragment reads of
+//    16 consecutive lanes (rows r .. r + 15) hit 16 distinct bank groups;
+//  - 4-bit weights: the 32 code bytes of each of the tile's 256 rows, read
+//    back by the lanes that expand them (row tables stay in registers);
+//    f16 weights: 128-byte rows swizzled like A.
+// The loads are issued from inline asm, so the compiler does not track them:
+// each wave waits for its own loads of a stage (vmcnt) and a workgroup
+// barrier follows before any use; nothing else in the loop reads global
+// memory. bf16 activations are converted to f16 in place after they land.
+// Both weight formats run the same MFMA sequence, so equal weight values give
+// bit-identical results. At the end group 1 hands its accumulators to group 0
+// through LDS; group 0 adds them (a fixed order) and runs the epilogue.
+template <int FM, bool LUT4>
+struct K2Shape {
+  // LDS stages (loads run NS - 1 k-tiles ahead); 4-bit tiles are small
+  // enough for four
+  static constexpr int NS = LUT4 ? 4 : 3;
+  static constexpr int A_BYTES = 32 * FM * BK * 2;                  // A of one k-tile
+  static constexpr int B_BYTES = LUT4 ? 256 * BK / 2 : 256 * BK * 2;  // weights of one k-tile
+  static constexpr int ST_BYTES = A_BYTES + B_BYTES;
+  static constexpr int A_INSTR = A_BYTES / 1024;                    // wave-level loads of A (= 4 FM)
+  static constexpr int B_INSTR = B_BYTES / 1024;                    // and of the weights (8 or 32)
+  static constexpr int A_HI = (A_INSTR + 7) / 8, A_LO = A_INSTR / 8;  // per wave (waves < A_INSTR % 8: A_HI)
+  static constexpr int B_PER = B_INSTR / 8;
+  static constexpr int HALF = (FM + 1) / 2;                         // row blocks exchanged per round
+  static constexpr size_t STAGES = (size_t)NS * ST_BYTES;
+  static constexpr size_t XCHG = (size_t)HALF * 4 * 2 * 16 * 64 * 4;
+  static constexpr size_t STAGING = (size_t)2 * 32 * 260 * 4;      // epilogue tiles of both groups
+  static constexpr size_t LDS0 = STAGES > XCHG ? STAGES : XCHG;
+  static constexpr size_t LDS = LDS0 > STAGING ? LDS0 : STAGING;
+};
+
+// global -> LDS, 16 bytes per lane: lane l's bytes at gbase + voff land at
+// LDS byte address lds + 16 l (gbase and lds wave-uniform). M0 carries the LDS
+// address; nothing else in the kernels using this relies on M0.
+__device__ inline void dma16(const void* gbase, uint32_t voff, uint32_t lds) {
+  // the base and the LDS address are wave-uniform by contract; readfirstlane
+  // puts them in scalar registers whatever the divergence analysis concluded
+  // (readfirstlane returns int: each half goes through uint32_t before it is
+  // widened, or a low half with bit 31 set would sign-extend into the high one)
+  const uint64_t g = (uint64_t)(uintptr_t)gbase;
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(g >> 32));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)g);
+  const uint64_t gs = ((uint64_t)hi << 32) | (uint64_t)lo;
+  const uint32_t ls = (uint32_t)__builtin_amdgcn_readfirstlane(lds);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(gs), "s"(ls) : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+// s_waitcnt with only vmcnt constrained (expcnt, lgkmcnt at their maxima)
+template <int N>
+__device__ inline void wait_vmcnt_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ inline uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// Epilogue of the two-group kernel. Each group finishes its row blocks one
+// 32-row block per round: the block's f32 sums go to the group's LDS staging
+// tile (32 x 256, rows padded to K2_XLD floats), then the group's 256 threads
+// apply the epilogue arithmetic of tile_epilogue / store_one element by
+// element and store 16-byte runs along the output's contiguous dimension: 8
+// columns of a row (row-major outputs, head-major q / k / relK rows), 8 rows of
+// a column (the transposed V), 4 GLU channels of a row (f32).
+constexpr int K2_XLD = 260;
+
+__device__ inline uint16_t bf16_bits(float v) {
+  uint32_t u = __float_as_uint(v);
+  u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite inputs)
+  return (uint16_t)(u >> 16);
+}
+
+// Stores staged block rows [0, 32) (global rows row0 ..) x tile columns [0, 256).
+template <int EPI>
+__device__ inline void k2_store_block(const float* xs, const GemmParams& p, int row0, int n0, int bz, int gt) {
+  const EpiArgs& ea = p.ea;
   if constexpr (EPI == (int)Epi::Glu) {
-    float* base = ea.out_f32 + (size_t)mrow * ea.ldo + (nw >> 1) + l32;
+    // output channel (n0 >> 1) + ch: value = column 64 (ch >> 5) + (ch & 31), gate = that + 32
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int k = 0; k < 4; ++k) {
+      const int q = gt + 256 * k, row = q >> 5, ch = (q & 31) * 4;
+      if (row0 + row >= p.M) continue;
+      const int cv = 64 * (ch >> 5) + (ch & 31);
+      const floatx4 a = *reinterpret_cast<const floatx4*>(xs + row * K2_XLD + cv);
+      const floatx4 g = *reinterpret_cast<const floatx4*>(xs + row * K2_XLD + cv + 32);
+      floatx4 o;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
-        if (row_ok(rl)) base[(size_t)rl * ea.ldo] = fast_sigmoid_mul(acc[i][0][v], acc[i][1][v]);
-      }
+      for (int e = 0; e < 4; ++e) o[e] = fast_sigmoid_mul(a[e], g[e]);
+      *reinterpret_cast<floatx4*>(ea.out_f32 + (size_t)(row0 + row) * ea.ldo + (n0 >> 1) + ch) = o;
+    }
   } else if constexpr (EPI == (int)Epi::Qkv) {
-    const int region = __builtin_amdgcn_readfirstlane(nw >> 10);  // 0 q, 1 k, 2 v (wave-uniform)
+    const int region = n0 >> 10;  // 0 q, 1 k, 2 v (a tile lies in one)
     if (region == 2) {
-      // V^T[h][d][r]: a lane's four consecutive rows are contiguous, one 8-byte store
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int hd = nw - 2048 + 32 * j + l32;  // h*128 + d
-        half* vrow = ea.vt + (size_t)hd * ea.mp + mrow;
+      for (int k = 0; k < 4; ++k) {
+        const int q = gt + 256 * k, c = q >> 2, r8 = (q & 3) * 8;
+        const int hd = n0 - 2048 + c;
+        half* dst = ea.vt + (size_t)hd * ea.mp + row0 + r8;
+        half8 o;
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+        for (int e = 0; e < 8; ++e) o[e] = to_f16(xs[(r8 + e) * K2_XLD + c]);
+        if (row0 + r8 + 7 < p.M) {
+          *reinterpret_cast<half8*>(dst) = o;
+        } else {
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int rl = 32 * i + 8 * g;
-            if (!CHK || mrow + rl + 3 < p.M) {
-              const half4 w4 = {to_f16(acc[i][j][4 * g]), to_f16(acc[i][j][4 * g + 1]),
-                                to_f16(acc[i][j][4 * g + 2]), to_f16(acc[i][j][4 * g + 3])};
-              *reinterpret_cast<half4*>(vrow + rl) = w4;
-            } else {
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (mrow + rl + e < p.M) vrow[rl + e] = to_f16(acc[i][j][4 * g + e]);
-            }
-          }
+          for (int e = 0; e < 8; ++e)
+            if (row0 + r8 + e < p.M) dst[e] = o[e];
+        }
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int hd = (nw & 1023) + 32 * j + l32, h = hd >> 7, d = hd & 127;
-        const size_t off = ((size_t)h * ea.mp + mrow) * HDIM + d;
+      for (int k = 0; k < 4; ++k) {
+        const int q = gt + 256 * k, row = q >> 5, c8 = (q & 31) * 8;
+        if (row0 + row >= p.M) continue;
+        const int hd = (n0 & 1023) + c8, h = hd >> 7, d = hd & 127;
+        const size_t off = ((size_t)h * ea.mp + row0 + row) * HDIM + d;
+        const floatx4 a = *reinterpret_cast<const floatx4*>(xs + row * K2_XLD + c8);
+        const floatx4 b = *reinterpret_cast<const floatx4*>(xs + row * K2_XLD + c8 + 4);
+        const float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
         if (region == 0) {
-          const float bu = ea.bu[hd], bv = ea.bv[hd];
-          half* pu = ea.qu + off;
-          half* pv = ea.qv + off;
+          half8 u, w;
 #pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
-              if (row_ok(rl)) {
-                pu[rl * HDIM] = to_f16((acc[i][j][v] + bu) * ea.scale);
-                pv[rl * HDIM] = to_f16((acc[i][j][v] + bv) * ea.scale);
-              }
-            }
+          for (int e = 0; e < 8; ++e) {
+            u[e] = to_f16((v[e] + ea.bu[hd + e]) * ea.scale);
+            w[e] = to_f16((v[e] + ea.bv[hd + e]) * ea.scale);
+          }
+          *reinterpret_cast<half8*>(ea.qu + off) = u;
+          *reinterpret_cast<half8*>(ea.qv + off) = w;
         } else {
-          half* pk = ea.kh + off;
+          half8 u;
 #pragma unroll
-          for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
-              if (row_ok(rl)) pk[rl * HDIM] = to_f16(acc[i][j][v]);
-            }
+          for (int e = 0; e < 8; ++e) u[e] = to_f16(v[e]);
+          *reinterpret_cast<half8*>(ea.kh + off) = u;
         }
       }
     }
-  } else if constexpr (EPI == (int)Epi::RelK) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int c = nw + 32 * j + l32, h = c >> 7, d = c & 127;
-      half* pr = ea.rk + ((size_t)h * ea.pp + mrow) * HDIM + d;
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
-          if (row_ok(rl)) pr[rl * HDIM] = to_f16(acc[i][j][v]);
-        }
-    }
-  } else if constexpr (EPI == (int)Epi::StoreF16 || EPI == (int)Epi::StoreBF16 || EPI == (int)Epi::Silu ||
-                       EPI == (int)Epi::BiasReluF16) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int c = nw + 32 * j + l32;
-      const float bc = ea.bias ? ea.bias[c] : 0.0f;
-      const size_t base = (size_t)mrow * ea.ldo + c;
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
-          if (!row_ok(rl)) continue;
-          const size_t at = base + (size_t)rl * ea.ldo;
-          const float x = acc[i][j][v];
-          if constexpr (EPI == (int)Epi::StoreF16) {
-            ea.out_f16[at] = to_f16(x + bc);
-          } else if constexpr (EPI == (int)Epi::StoreBF16) {
-            uint32_t u = __float_as_uint(x + bc);
-            u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite inputs)
-            reinterpret_cast<uint16_t*>(ea.out_f16)[at] = (uint16_t)(u >> 16);
-          } else if constexpr (EPI == (int)Epi::Silu) {
-            ea.out_f16[at] = to_f16(fast_sigmoid_mul(x, x));
-          } else {
-            const float y = x + bc;
-            ea.out_f16[at] = to_f16(y > 0.0f ? y : 0.0f);
-          }
-        }
-    }
   } else {
+    // row-major outputs and relK (head-major rows): 8 columns of a row
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int k = 0; k < 4; ++k) {
+      const int q = gt + 256 * k, row = q >> 5, c8 = (q & 31) * 8;
+      if (row0 + row >= p.M) continue;
+      const int grow = row0 + row, col = n0 + c8;
+      const floatx4 a = *reinterpret_cast<const floatx4*>(xs + row * K2_XLD + c8);
+      const floatx4 b = *reinterpret_cast<const floatx4*>(xs + row * K2_XLD + c8 + 4);
+      float v[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+      if constexpr (EPI == (int)Epi::StoreF32) {
+        float* dst = ea.out_f32 + bz * p.out_zstride + (size_t)grow * ea.ldo + col;
+        if (ea.bias) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] += ea.bias[col + e];
+        }
+        *reinterpret_cast<floatx4*>(dst) = floatx4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<floatx4*>(dst + 4) = floatx4{v[4], v[5], v[6], v[7]};
+      } else if constexpr (EPI == (int)Epi::StoreF16 || EPI == (int)Epi::Silu) {
+        half8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if constexpr (EPI == (int)Epi::Silu) o[e] = to_f16(fast_sigmoid_mul(v[e], v[e]));
+          else o[e] = to_f16(ea.bias ? v[e] + ea.bias[col + e] : v[e]);
+        }
+        *reinterpret_cast<half8*>(ea.out_f16 + (size_t)grow * ea.ldo + col) = o;
+      } else if constexpr (EPI == (int)Epi::StoreBF16) {
+        uint16_t o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = bf16_bits(ea.bias ? v[e] + ea.bias[col + e] : v[e]);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(ea.out_f16) + (size_t)grow * ea.ldo + col) =
+            *reinterpret_cast<const uint4*>(o);
+      } else if constexpr (EPI == (int)Epi::RelK) {
+        const int h = col >> 7, d = col & 127;
+        half8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = to_f16(v[e]);
+        *reinterpret_cast<half8*>(ea.rk + ((size_t)h * ea.pp + grow) * HDIM + d) = o;
+      }
+    }
+  }
+}
+
+template <int FM, bool LUT4, bool SWZ, bool ABF16, int EPI>
+__global__ void __launch_bounds__(512, 1) gemm_k2_kernel(GemmParams p) {
+  using S = K2Shape<FM, LUT4>;
+  constexpr int NS = S::NS;
+  extern __shared__ __attribute__((aligned(16))) unsigned char k2_lds[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave 0..7
+  const int grp = wv >> 2, w = wv & 3;
+  const int l32 = lane & 31, lhi = lane >> 5;
+  // XCD-aware tile order, as gemm_wide_kernel
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int G = gx * gy * gridDim.z;
+  const int bid = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const int xq = G / 8, xr = G % 8, xcd = bid % 8;
+  const int tix = xcd * xq + min(xcd, xr) + bid / 8;
+  const int bz = tix / (gx * gy), by = (tix / gx) % gy, bx = tix % gx;
+  const int n0 = bx * 256, m0 = by * 32 * FM;
+  const int nw = n0 + w * 64;
+  const int kunits = p.K / 256, kq = kunits / p.splits, kr = kunits % p.splits;
+  const int kz0 = 256 * (bz * kq + min(bz, kr));
+  const int nk = 4 * (kq + (bz < kr ? 1 : 0));  // k-tiles of this split
+
+  // this lane's row tables, complete before any load is issued (the compiler
+  // only knows of these loads)
+  RowLut lut[2];
+  if constexpr (LUT4) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) lut[j] = load_row_lut(p.lut + (size_t)(nw + 32 * j + l32) * 16);
+  }
+  wait_vmcnt_le<0>();
+
+  // Load sources. Wave-level load d of a k-tile writes LDS bytes 1024 d ..
+  // of the stage, chunk ch = 64 d + lane: A row ch >> 3 at position ch & 7,
+  // holding global chunk (ch & 7) ^ ((row >> 1) & 7) (rows past M repeat row M - 1,
+  // never stored). Wave wv issues A loads d = wv, wv + 8, ... and weight loads
+  // d = wv + 8 t (t < B_PER): 4-bit, chunk P = 64 d + lane is row P >> 1, code
+  // bytes 16 (P & 1) .. of the row's 32; f16, row ch >> 3 like A.
+  const int a_my = wv < S::A_INSTR % 8 ? S::A_HI : S::A_LO;
+  const half* abase = p.A + (size_t)m0 * p.lda + kz0;
+  uint32_t aoff[S::A_HI];
+#pragma unroll
+  for (int t = 0; t < S::A_HI; ++t) {
+    const int ch = 64 * (wv + 8 * t) + lane, row = min(ch >> 3, 32 * FM - 1), cc = (ch & 7) ^ ((row >> 1) & 7);
+    aoff[t] = ((uint32_t)min(row, p.M - 1 - m0) * (uint32_t)p.lda + cc * 8) * 2u;
+  }
+  const uint8_t* bbase = LUT4 ? p.codes + (size_t)n0 * (p.K / 2) + kz0 / 2
+                              : reinterpret_cast<const uint8_t*>(p.W + (size_t)n0 * p.K + kz0);
+  uint32_t boff[S::B_PER];
+#pragma unroll
+  for (int t = 0; t < S::B_PER; ++t) {
+    const int ch = 64 * (wv + 8 * t) + lane;
+    if constexpr (LUT4) {
+      boff[t] = (uint32_t)(ch >> 1) * (uint32_t)(p.K / 2) + 16 * (ch & 1);
+    } else {
+      const int row = ch >> 3, cc = (ch & 7) ^ ((row >> 1) & 7);
+      boff[t] = ((uint32_t)row * (uint32_t)p.K + cc * 8) * 2u;
+    }
+  }
+  const uint32_t lds0 = lds_addr(k2_lds);
+
+  // k-tile kt into stage st (loads past the last k-tile re-read it: in
+  // bounds, and their stage is never read)
+  auto issue = [&](int kt, int st) {
+    kt = min(kt, nk - 1);
+    const uint32_t sb = lds0 + st * S::ST_BYTES;
+    const half* at = abase + kt * BK;
+#pragma unroll
+    for (int t = 0; t < S::A_HI; ++t)
+      if (t < a_my) dma16(at, aoff[t], sb + (wv + 8 * t) * 1024);
+    const uint8_t* bt = bbase + (size_t)kt * (LUT4 ? BK / 2 : BK * 2);
+#pragma unroll
+    for (int t = 0; t < S::B_PER; ++t) dma16(bt, boff[t], sb + S::A_BYTES + (wv + 8 * t) * 1024);
+  };
+  // a wave waits for its own loads of the oldest stage in flight: those of
+  // the NS - 2 k-tiles issued after them may stay outstanding
+  auto wait_stage = [&]() {
+    if (wv < S::A_INSTR % 8) wait_vmcnt_le<(NS - 2) * (S::A_HI + S::B_PER)>();
+    else wait_vmcnt_le<(NS - 2) * (S::A_LO + S::B_PER)>();
+  };
+  // bf16 activations: each wave converts the A chunks it loaded, in place
+  auto convert_a = [&](int st) {
+    if constexpr (ABF16) {
+      half* a = reinterpret_cast<half*>(k2_lds + st * S::ST_BYTES);
+#pragma unroll
+      for (int t = 0; t < S::A_HI; ++t) {
+        if (t >= a_my) continue;
+        half* c = a + (64 * (wv + 8 * t) + lane) * 8;
+        const uint4 u = *reinterpret_cast<const uint4*>(c);
+        const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+        half8 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[2 * e] = (half)__uint_as_float(w4[e] << 16);
+          v[2 * e + 1] = (half)__uint_as_float(w4[e] & 0xffff0000u);
+        }
+        st_half8(c, v);
+      }
+    }
+  };
+
+  floatx16 acc[FM][2];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const int arow_sw = (l32 >> 1) & 7;
+  // Fragments of this group's two slices of one k-tile: A (both slices) and
+  // the weights, 4-bit codes expanded to f16 — read and expanded in one phase,
+  // multiplied in the next.
+  half8 af[2][FM], bf[2][2];
+  auto load_frags = [&](int st) {
+    const unsigned char* sb = k2_lds + st * S::ST_BYTES;
+    const half* a = reinterpret_cast<const half*>(sb);
+    const unsigned char* bw = sb + S::A_BYTES;
+    uint2 cw[2];
+    if constexpr (LUT4) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
+        cw[j] = *reinterpret_cast<const uint2*>(bw + ((w * 64 + 32 * j + l32) * 2 + lhi) * 16 + 8 * grp);
+    }
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int r = m0 + i * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
-          if (r < p.M) store_one<EPI>(ea, r, nw + 32 * j + l32, acc[i][j][v]);
+    for (int ss = 0; ss < 2; ++ss) {
+      const int s = 2 * grp + ss;
+      const half* ar = a + l32 * BK + (((4 * lhi + s) ^ arow_sw) * 8);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[ss][i] = ld_half8(ar + i * 32 * BK);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if constexpr (LUT4) {
+          const uint4 q = expand8<SWZ>(ss == 0 ? cw[j].x : cw[j].y, lut[j]);
+          bf[ss][j] = *reinterpret_cast<const half8*>(&q);
+        } else {
+          const int col = w * 64 + 32 * j + l32;
+          bf[ss][j] = ld_half8(reinterpret_cast<const half*>(bw) + col * BK + (((4 * lhi + s) ^ ((col >> 1) & 7)) * 8));
         }
-  }
+      }
+    }
   };
-  // a tile inside M skips every per-row check (the f32 store, the split-K
-  // partial, measured faster with the checks kept: one code path)
-  if constexpr (EPI == (int)Epi::StoreF32 || EPI == (int)Epi::FlattenReluF16) epilogue(std::integral_constant<bool, true>());
-  else if (m0 + BM <= p.M) epilogue(std::integral_constant<bool, false>());
-  else epilogue(std::integral_constant<bool, true>());
+  auto mfma_all = [&]() {
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ss][i], bf[ss][j], acc[i][j], 0, 0, 0);
+  };
+
+  // Ping-pong: the two waves of a SIMD run opposite phases. In phase 1 of
+  // k-tile t group 0 multiplies tile t (fragments prepared in the phase
+  // before) while group 1 reads and expands tile t; in phase 2 group 1
+  // multiplies tile t while group 0 prepares tile t + 1. So one wave's MFMAs
+  // overlap the other's LDS reads and code expansion. During phase 1 every
+  // wave issues its loads of tile t + 2 into the stage tile t - 1 occupied
+  // (both groups finished with it by the barrier that ended the previous
+  // k-tile), then waits for its own loads of tile t + 1; the barrier after
+  // phase 1 makes tile t + 1 visible to all waves for the reads of phase 2.
+  // (the group is a template constant in each copy of the loop, so the
+  // compiler sees when the fragments are dead; both copies execute the same
+  // barriers)
+  auto pingpong = [&](auto gconst) {
+    constexpr int G = decltype(gconst)::value;
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t) issue(t, t);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_stage();
+    __builtin_amdgcn_s_barrier();
+    if constexpr (ABF16) {
+      convert_a(0);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_s_barrier();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (G == 0) load_frags(0);
+    for (int kt = 0; kt < nk; ++kt) {
+      const int st = kt % NS;
+      __builtin_amdgcn_sched_barrier(0);
+      // phase 1
+      if constexpr (G == 0) mfma_all();
+      else load_frags(st);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(kt + NS - 1, (kt + NS - 1) % NS);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_stage();
+      __builtin_amdgcn_s_barrier();
+      if constexpr (ABF16) {
+        if (kt + 1 < nk) convert_a((kt + 1) % NS);
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_s_barrier();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // phase 2
+      if constexpr (G == 1) mfma_all();
+      else if (kt + 1 < nk) load_frags((kt + 1) % NS);
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+    }
+  };
+  if (grp == 0) pingpong(std::integral_constant<int, 0>());
+  else pingpong(std::integral_constant<int, 1>());
+  wait_vmcnt_le<0>();
+  __syncthreads();  // every load landed and every wave is done with the stages
+
+  // The two groups' sums are combined through LDS and both groups finish
+  // the tile: group 0 the row blocks [0, H0), group 1 the rest. Round 0: group
+  // 1 hands over its blocks [0, H0); round 1: group 0 its blocks [H0, FM).
+  // (acc_g0 + acc_g1 either way: the addition commutes exactly.)
+  float* xb = reinterpret_cast<float*>(k2_lds);
+  constexpr int H0 = S::HALF;
+  auto xaddr = [&](int bi, int j, int q) { return xb + (((((w * H0 + bi) * 2 + j) * 4 + q) * 64 + lane) * 4); };
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int i0 = r == 0 ? 0 : H0, i1 = r == 0 ? H0 : FM;
+    if (grp == 1 - r) {  // sender
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        if (i < i0 || i >= i1) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const floatx4 v4 = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            *reinterpret_cast<floatx4*>(xaddr(i - i0, j, q)) = v4;
+          }
+      }
+    }
+    __syncthreads();
+    if (grp == r) {  // receiver
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        if (i < i0 || i >= i1) continue;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const floatx4 v4 = *reinterpret_cast<const floatx4*>(xaddr(i - i0, j, q));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += v4[e];
+          }
+      }
+    }
+    if (r == 0) __syncthreads();
+  }
+  // Per-element epilogue (both groups at once, each on its blocks), except
+  // the transposed V of the qkv projection: its 16-byte runs go down a column,
+  // so those tiles are staged through LDS one 32-row block per round.
+  if constexpr (EPI == (int)Epi::Qkv) {
+    if (n0 >= 2048) {
+      __syncthreads();  // the exchange area is reused for staging
+      float* xs = xb + grp * 32 * K2_XLD;
+      const int gt = w * 64 + lane;
+#pragma unroll
+      for (int r = 0; r < H0; ++r) {
+        const int bi = grp == 0 ? r : H0 + r;  // this group's block of the round
+        const bool active = bi < FM;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          if (i != bi) continue;
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              xs[(8 * (v >> 2) + 4 * lhi + (v & 3)) * K2_XLD + 64 * w + 32 * j + l32] = acc[i][j][v];
+        }
+        __syncthreads();
+        if (active) k2_store_block<EPI>(xs, p, m0 + 32 * bi, n0, bz, gt);
+        __syncthreads();
+      }
+      return;
+    }
+  }
+  if (grp == 0) tile_epilogue<FM, EPI>(acc, p, m0, nw, bz, lane, 0, H0);
+  else tile_epilogue<FM, EPI>(acc, p, m0, nw, bz, lane, H0, FM);
 }
+
 
 // out[r][c] = sum_s part[s][r][c] (s ascending), stored as f32 / f16 / bf16
 // (out_kind 0 / 1 / 2, bf16 rounded to nearest even). Four columns per thread.
@@ -836,6 +1322,128 @@ void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t 
 #undef BARK_CASE
 #undef BARK_K
   throw Error{"gemm: no wide kernel for this epilogue and weight format"};
+}
+
+// The two-group kernel's instances: the encoder's epilogues on f16 weights
+// (fmt 0) and on swizzled 4-bit weights (fmt 1) — the same kernel for both, so
+// equal weight values give equal results; plain stores on plain 4-bit codes
+// (fmt 2) with f16 or bf16 activations (the isolated linear).
+bool k2_supported(Epi epi, int fmt) {
+  if (fmt == 2) return epi == Epi::StoreF32 || epi == Epi::StoreF16 || epi == Epi::StoreBF16;
+  switch (epi) {
+    case Epi::StoreF32:
+    case Epi::Silu:
+    case Epi::Glu:
+    case Epi::Qkv:
+    case Epi::RelK:
+      return true;
+    default:
+      return false;
+  }
+}
+
+template <int FM, int EPI, bool L4, bool SW, bool AB>
+void launch_k2_one(const GemmParams& p, hipStream_t s) {
+  auto kern = gemm_k2_kernel<FM, L4, SW, AB, EPI>;
+  constexpr size_t lds = K2Shape<FM, L4>::LDS;
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  static const bool attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess;
+  BARK_REQUIRE(attr, "gemm: cannot reserve LDS for the two-group kernel");
+  dim3 grid(p.N / 256, ceil_div(p.M, 32 * FM), p.splits), block(512);
+  BARK_LAUNCH(kern, grid, block, lds, s, p);
+}
+
+template <int FM>
+void launch_k2(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t s) {
+#define BARK_KE(E)                                                      \
+  case Epi::E:                                                          \
+    if (fmt == 1) launch_k2_one<FM, (int)Epi::E, true, true, false>(p, s);   \
+    else launch_k2_one<FM, (int)Epi::E, false, false, false>(p, s);         \
+    return;
+#define BARK_KP(E)                                                      \
+  case Epi::E:                                                          \
+    if constexpr (FM <= 4) {                                            \
+      if (abf16) {                                                      \
+        launch_k2_one<FM, (int)Epi::E, true, false, true>(p, s);        \
+        return;                                                         \
+      }                                                                 \
+    }                                                                   \
+    launch_k2_one<FM, (int)Epi::E, true, false, false>(p, s);           \
+    return;
+  if (fmt == 2) {
+    switch (epi) {
+      BARK_KP(StoreF32)
+      BARK_KP(StoreF16)
+      BARK_KP(StoreBF16)
+      default:
+        break;
+    }
+  } else {
+    switch (epi) {
+      BARK_KE(StoreF32)
+      BARK_KE(Silu)
+      BARK_KE(Glu)
+      BARK_KE(Qkv)
+      BARK_KE(RelK)
+      default:
+        break;
+    }
+  }
+#undef BARK_KE
+#undef BARK_KP
+  throw Error{"gemm: no two-group kernel for this epilogue and weight format"};
+}
+
+// Whether an epilogue runs on the two-group kernel by default. Measured on
+// MI355X at T = 2207 (encoder step, per-op events): the FFN up projection
+// (SiLU, N = 4096) is 3-9 % faster; the other linears are within a few
+// percent either way, where the end-of-kernel store burst and the k-loop
+// overhead bound both kernels alike, so they stay on gemm_wide_kernel. The
+// choice depends on the epilogue only, so a weight's 4-bit and f16 forms
+// always run the same kernel. BARK_HIP_GEMM_K2 = 1 uses it for every
+// supported epilogue.
+bool k2_default(Epi epi) {
+  static const int forced = [] {
+    const char* e = getenv("BARK_HIP_GEMM_K2");
+    return e ? atoi(e) : -1;
+  }();
+  if (forced >= 1) return true;
+  if (forced == 0) return false;
+  return epi == Epi::Silu;
+}
+
+// Tile height (32-row blocks) of the two-group kernel: the height whose tile
+// count fills the 256 CUs best (one workgroup per CU), taller on ties.
+// BARK_HIP_GEMM_K2 = 0 disables the kernel, 3/4/5 forces a height.
+int pick_k2_fm(int M, int N, int splits) {
+  static const int forced = [] {
+    const char* e = getenv("BARK_HIP_GEMM_K2");
+    return e ? atoi(e) : -1;
+  }();
+  if (forced == 0) return 0;
+  if (forced >= 3 && forced <= 5) return forced;
+  constexpr int CUS = 256;
+  int best = 4;
+  double best_score = -1.0;
+  const int fms[3] = {3, 4, 5};
+  const double rate[3] = {0.95, 1.0, 1.05};
+  for (int i = 0; i < 3; ++i) {
+    const long tiles = (long)ceil_div(M, 32 * fms[i]) * (N / 256) * splits;
+    const long rounds = (tiles + CUS - 1) / CUS;
+    const double score = (double)tiles / (double)(CUS * rounds) * rate[i];
+    if (score > best_score + 1e-9) {
+      best_score = score;
+      best = fms[i];
+    }
+  }
+  return best;
+}
+
+void launch_k2_fm(int fm, const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t s) {
+  if (fm == 5 && !abf16) launch_k2<5>(p, epi, fmt, abf16, s);
+  else if (fm == 3) launch_k2<3>(p, epi, fmt, abf16, s);
+  else launch_k2<4>(p, epi, fmt, abf16, s);
 }
 
 // Full epilogue set: f16 weights and swizzled 4-bit weights (the encoder).
@@ -943,6 +1551,14 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   BARK_REQUIRE(!a_bf16 || (W.lut4() && !W.swizzled), "gemm: bf16 activations need plain 4-bit weights");
   const bool fits32 = (double)M * lda * 2 < 4.0e9 && (double)W.n * W.k * 2 < 4.0e9;
   const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
+  if (W.n % 256 == 0 && fits32 && W.k / BK >= 4 && k2_supported(epi, fmt) && k2_default(epi)) {
+    const int fm2 = pick_k2_fm(M, W.n, 1);
+    if (fm2) {
+      launch_k2_fm(fm2, p, epi, fmt, a_bf16, stream);
+      BARK_HIP_CHECK(hipGetLastError());
+      return;
+    }
+  }
   const int fm = W.n % 256 == 0 && fits32 && wide_supported(epi, fmt) ? pick_wide_fm(M, W.n, W.k) : 0;
   if (fm) {
     if (fm == 8) launch_wide<8>(p, epi, fmt, a_bf16, stream);
@@ -979,6 +1595,14 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
   ea.ldo = ldo;
   GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, splits, (size_t)M * ldo};
   const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
+  if (k2_default(Epi::StoreF32)) {
+    const int fm2 = pick_k2_fm(M, W.n, splits);
+    if (fm2) {
+      launch_k2_fm(fm2, p, Epi::StoreF32, fmt, a_bf16, stream);
+      BARK_HIP_CHECK(hipGetLastError());
+      return;
+    }
+  }
   int fm = pick_wide_fm(M, W.n, W.k, splits);
   if (fm == 0) fm = 2;
   if (fm == 8) launch_wide<8>(p, Epi::StoreF32, fmt, a_bf16, stream);
@@ -1031,13 +1655,12 @@ float* isolated_workspace(hipStream_t stream, size_t bytes) {
 }
 }  // namespace
 
-void gemm_isolated(const half* A, int M, const GemmWeight& W, void* C, int c_kind, hipStream_t stream,
-                   bool a_bf16) {
-  BARK_REQUIRE(c_kind >= 0 && c_kind <= 2, "gemm_isolated: bad output kind");
-  // Split K when the output tiles alone leave most CUs idle: at small T as
-  // far as the CUs fill, and in two for a long K whose 128-row tiles cover
-  // fewer than half of them (T = 2207, K = 4096, N = 1024). The chunks'
-  // partial sums go to a workspace and one pass adds them in order.
+namespace {
+// K splits of the isolated linear: split K when the output tiles alone leave
+// most CUs idle, at small T as far as the CUs fill, and in two for a long K
+// whose 128-row tiles cover fewer than half of them (T = 2207, K = 4096,
+// N = 1024). A function of (M, N, K) only.
+int isolated_splits(int M, const GemmWeight& W) {
   const long base = (long)ceil_div(M, 64) * (W.n / 256);
   int splits = 1;
   if (W.n % 256 == 0 && base < 128) {
@@ -1045,6 +1668,15 @@ void gemm_isolated(const half* A, int M, const GemmWeight& W, void* C, int c_kin
   } else if (W.n % 256 == 0 && W.k >= 2048 && W.k % 512 == 0 && (long)ceil_div(M, 128) * (W.n / 256) < 128) {
     splits = 2;
   }
+  return splits;
+}
+
+// The isolated linear with its partial sums in `part` (bytes available:
+// part_bytes), or in the grow-only per-stream workspace when part is null.
+void isolated_with(const half* A, int M, const GemmWeight& W, void* C, int c_kind, hipStream_t stream,
+                   bool a_bf16, float* part, size_t part_bytes) {
+  BARK_REQUIRE(c_kind >= 0 && c_kind <= 2, "gemm_isolated: bad output kind");
+  const int splits = isolated_splits(M, W);
   if (splits == 1) {
     EpiArgs e;
     e.ldo = W.n;
@@ -1058,13 +1690,29 @@ void gemm_isolated(const half* A, int M, const GemmWeight& W, void* C, int c_kin
     gemm(A, W.k, M, W, epi, e, stream, a_bf16);
     return;
   }
+  // the chunks' partial sums go to the workspace and one pass adds them in order
   const size_t stride = (size_t)M * W.n;
-  float* part = isolated_workspace(stream, splits * stride * sizeof(float));
+  const size_t need = splits * stride * sizeof(float);
+  if (part) {
+    BARK_REQUIRE(need <= part_bytes,
+                 "gemm_isolated: partial-sum buffer too small: " + std::to_string(need) + " bytes needed, " +
+                     std::to_string(part_bytes) + " given");
+  } else {
+    part = isolated_workspace(stream, need);
+  }
   gemm_split(A, W.k, M, W, splits, part, W.n, stream, a_bf16);
   const long n4 = (long)(stride / 4);
   BARK_LAUNCH(split_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream, part,
                      splits, stride, C, c_kind, n4);
   BARK_HIP_CHECK(hipGetLastError());
 }
+}  // namespace
+
+void gemm_isolated(const half* A, int M, const GemmWeight& W, void* C, int c_kind, hipStream_t stream,
+                   bool a_bf16) {
+  isolated_with(A, M, W, C, c_kind, stream, a_bf16, nullptr, 0);
+}
+
+
 
 }  // namespace bark

@@ -70,9 +70,11 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
 void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, float* part,
                 int ldo, hipStream_t stream, bool a_bf16 = false);
 // The isolated linear C (M x N, dense) = A (M x K, lda = K) . W^T with output
-// kind 0 = f32, 1 = f16, 2 = bf16; splits K over a workspace when M is small.
+// kind 0 = f32, 1 = f16, 2 = bf16; splits K over a workspace when M is small
+// (grow-only, per stream, allocated on first need).
 void gemm_isolated(const half* A, int M, const GemmWeight& W, void* C, int c_kind, hipStream_t stream,
                    bool a_bf16);
+
 // Split-K count for the residual linears, a function of (N, K) only.
 int residual_splits(int n, int k);
 
