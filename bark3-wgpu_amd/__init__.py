@@ -40,6 +40,7 @@ __all__ = [
     "lib",
     "lib_path",
     "lowbit_linear",
+    "lowbit_linear_noalloc",
     "tensor_names",
     "conv_len",
     "HEADER_SYMBOLS",
@@ -178,6 +179,13 @@ _SIGS = {
     "bark_hip_profile_only": (_c.c_int, [_c.c_void_p, _c.c_char_p]),
     "bark_hip_profile_report": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_size_t]),
     "bark_hip_lowbit_linear": (
+        _c.c_int,
+        [
+            _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int32,
+            _c.c_int32, _c.c_int32, _c.c_int32, _c.c_void_p,
+        ],
+    ),
+    "bark_hip_lowbit_linear_noalloc": (
         _c.c_int,
         [
             _c.c_void_p, _c.c_int32, _c.c_void_p, _c.c_void_p, _c.c_void_p, _c.c_int32,
@@ -545,6 +553,19 @@ class HipEncoder:
 
     def __exit__(self, *exc):
         self.close()
+
+
+def lowbit_linear_noalloc(A: int, a_dtype: int, codes: int, lut16: int, C: int, c_dtype: int, T: int, K: int,
+                          N: int, stream: int = 0) -> None:
+    """bark_hip_lowbit_linear_noalloc: the isolated linear without any device
+    allocation (partial sums in a fixed per-GPU array; calls that overlap on
+    one GPU race)."""
+    _check(
+        lib().bark_hip_lowbit_linear_noalloc(
+            ctypes.c_void_p(A), a_dtype, ctypes.c_void_p(codes), ctypes.c_void_p(lut16), ctypes.c_void_p(C), c_dtype,
+            T, K, N, ctypes.c_void_p(stream) if stream else None,
+        )
+    )
 
 
 def lowbit_linear(A: int, a_dtype: int, codes: int, lut16: int, C: int, c_dtype: int, T: int, K: int, N: int,

@@ -1206,7 +1206,7 @@ HostTensor& stage(BarkHip* h, const char* name) {
 
 namespace {
 void lowbit_linear_checked(const void* A, int32_t a_dtype, const uint8_t* codes, const uint16_t* lut16, void* C,
-                           int32_t c_dtype, int32_t T, int32_t K, int32_t N, void* stream) {
+                           int32_t c_dtype, int32_t T, int32_t K, int32_t N, void* stream, bool noalloc) {
   BARK_REQUIRE(A && codes && lut16 && C, "null device pointer");
   BARK_REQUIRE(a_dtype == 0 || a_dtype == 1, "a_dtype must be 0 (f16) or 1 (bf16)");
   BARK_REQUIRE(c_dtype >= 0 && c_dtype <= 2, "c_dtype must be 0, 1 or 2");
@@ -1218,7 +1218,11 @@ void lowbit_linear_checked(const void* A, int32_t a_dtype, const uint8_t* codes,
   w.k = K;
   BARK_REQUIRE(K % 256 == 0 && K > 0, "K must be a positive multiple of 256");
   BARK_REQUIRE(N % 128 == 0 && N > 0, "N must be a positive multiple of 128");
-  gemm_isolated(static_cast<const half*>(A), T, w, C, c_dtype, static_cast<hipStream_t>(stream), a_dtype == 1);
+  if (noalloc)
+    gemm_isolated_noalloc(static_cast<const half*>(A), T, w, C, c_dtype, static_cast<hipStream_t>(stream),
+                          a_dtype == 1);
+  else
+    gemm_isolated(static_cast<const half*>(A), T, w, C, c_dtype, static_cast<hipStream_t>(stream), a_dtype == 1);
 }
 }  // namespace
 
@@ -1606,11 +1610,15 @@ int bark_hip_profile_report(BarkHip* h, char* buf, size_t cap) {
 }
 
 
+int bark_hip_lowbit_linear_noalloc(const void* A, int32_t a_dtype, const uint8_t* codes, const uint16_t* lut16,
+                                   void* C, int32_t c_dtype, int32_t T, int32_t K, int32_t N, void* stream) {
+  return guarded([&] { lowbit_linear_checked(A, a_dtype, codes, lut16, C, c_dtype, T, K, N, stream, true); });
+}
 
 int bark_hip_lowbit_linear(const void* A, int32_t a_dtype, const uint8_t* codes,
                            const uint16_t* lut16, void* C, int32_t c_dtype, int32_t T,
                            int32_t K, int32_t N, void* stream) {
-  return guarded([&] { lowbit_linear_checked(A, a_dtype, codes, lut16, C, c_dtype, T, K, N, stream); });
+  return guarded([&] { lowbit_linear_checked(A, a_dtype, codes, lut16, C, c_dtype, T, K, N, stream, false); });
 }
 
 }  // extern "C"

@@ -1656,6 +1656,32 @@ float* isolated_workspace(hipStream_t stream, size_t bytes) {
 }  // namespace
 
 namespace {
+// Partial sums of the no-allocation isolated linear: a file-scope device
+// array, one copy per GPU (each GPU the library runs on holds it until the
+// process ends). Host code must never hand its name to a kernel: in host code
+// it is a stand-in, not a device address; scratch_ptr() looks up the real one.
+static __device__ __align__(256) float scratch[ISOLATED_SCRATCH_BYTES / sizeof(float)];
+
+// Device address of `scratch` on the current device, looked up once per
+// device with hipGetSymbolAddress while that device is current; later calls
+// reuse it. No allocation is involved (a fixed table, no containers).
+float* scratch_ptr() {
+  constexpr int MAX_DEVICES = 64;
+  static std::mutex mu;
+  static float* ptrs[MAX_DEVICES] = {};
+  int dev = 0;
+  BARK_HIP_CHECK(hipGetDevice(&dev));
+  BARK_REQUIRE(dev >= 0 && dev < MAX_DEVICES, "scratch: device index out of range");
+  std::lock_guard<std::mutex> lk(mu);
+  if (!ptrs[dev]) {
+    void* ptr = nullptr;
+    BARK_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    BARK_REQUIRE(ptr != nullptr, "scratch: no device address");
+    ptrs[dev] = static_cast<float*>(ptr);
+  }
+  return ptrs[dev];
+}
+
 // K splits of the isolated linear: split K when the output tiles alone leave
 // most CUs idle, at small T as far as the CUs fill, and in two for a long K
 // whose 128-row tiles cover fewer than half of them (T = 2207, K = 4096,
@@ -1695,8 +1721,9 @@ void isolated_with(const half* A, int M, const GemmWeight& W, void* C, int c_kin
   const size_t need = splits * stride * sizeof(float);
   if (part) {
     BARK_REQUIRE(need <= part_bytes,
-                 "gemm_isolated: partial-sum buffer too small: " + std::to_string(need) + " bytes needed, " +
-                     std::to_string(part_bytes) + " given");
+                 "T x N too large for the fixed scratch of the no-allocation linear: it needs " +
+                     std::to_string(need) + " bytes of partial sums, the limit is " + std::to_string(part_bytes) +
+                     " (use bark_hip_lowbit_linear)");
   } else {
     part = isolated_workspace(stream, need);
   }
@@ -1713,6 +1740,10 @@ void gemm_isolated(const half* A, int M, const GemmWeight& W, void* C, int c_kin
   isolated_with(A, M, W, C, c_kind, stream, a_bf16, nullptr, 0);
 }
 
+void gemm_isolated_noalloc(const half* A, int M, const GemmWeight& W, void* C, int c_kind, hipStream_t stream,
+                           bool a_bf16) {
+  isolated_with(A, M, W, C, c_kind, stream, a_bf16, scratch_ptr(), ISOLATED_SCRATCH_BYTES);
+}
 
 
 }  // namespace bark

@@ -74,7 +74,13 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
 // (grow-only, per stream, allocated on first need).
 void gemm_isolated(const half* A, int M, const GemmWeight& W, void* C, int c_kind, hipStream_t stream,
                    bool a_bf16);
-
+// The same kernels and results without any allocation: the partial sums live
+// in a fixed device array of ISOLATED_SCRATCH_BYTES per GPU (shared by every
+// call on that GPU: calls that overlap on one GPU race); larger splits are
+// rejected.
+constexpr size_t ISOLATED_SCRATCH_BYTES = (size_t)24 << 20;
+void gemm_isolated_noalloc(const half* A, int M, const GemmWeight& W, void* C, int c_kind, hipStream_t stream,
+                           bool a_bf16);
 // Split-K count for the residual linears, a function of (N, K) only.
 int residual_splits(int n, int k);
 

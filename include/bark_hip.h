@@ -218,6 +218,20 @@ int bark_hip_lowbit_linear(const void *A, int32_t a_dtype, const uint8_t *codes,
                            const uint16_t *lut16, void *C, int32_t c_dtype, int32_t T,
                            int32_t K, int32_t N, void *stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): bark_hip_lowbit_linear with the same arguments, kernels
+ * and results, which calls no allocating routine. Where that entry point
+ * splits K over a grow-only workspace (small T, or a long K), this one keeps
+ * the partial sums in a fixed device array of 24 MiB per GPU, held from the
+ * first call on a GPU until the process ends; a shape whose partial sums need
+ * more (split count x T x N x 4 bytes) is rejected with BARK_HIP_EINVAL. Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (on
+ * different streams) race and must be ordered by the caller. */
+int bark_hip_lowbit_linear_noalloc(const void *A, int32_t a_dtype, const uint8_t *codes,
+                                   const uint16_t *lut16, void *C, int32_t c_dtype, int32_t T,
+                                   int32_t K, int32_t N, void *stream);
+
 /* Log-mel front end, the counterpart of MelFrontend (src/mel.rs:10-140).
  * bark_hip_set_mel_filters takes the 128 x 257 row-major f32 filterbank, as
  * MelFrontend::new does (src/mel.rs:25; the reference loads it from
