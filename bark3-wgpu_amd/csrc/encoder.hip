@@ -765,8 +765,8 @@ struct BarkHip {
     ensure(attn_lanes, ll.size() * sizeof(int));
     ensure(merges, std::max<size_t>(ml.size(), 1) * sizeof(int4));
     if (!ml.empty()) {
-      ensure(attn_po, tl.size() * HEADS * 128 * HDIM * 4);
-      ensure(attn_pml, tl.size() * HEADS * 128 * 2 * 4);
+      ensure(attn_po, tl.size() * HEADS * attention_query_tile() * HDIM * 2);
+      ensure(attn_pml, tl.size() * HEADS * attention_query_tile() * 2 * 4);
     }
     ensure_pos(pl.tc);
   }
@@ -778,8 +778,9 @@ struct BarkHip {
   // merge entry joins them when there is more than one.
   static void attention_tables(const Plan& pl, std::vector<int4>& tl, std::vector<int>& ll,
                                std::vector<int4>& ml) {
+    const int bq = attention_query_tile();
     for (const auto& s : pl.seqs) {
-      const int ntk = (s.t + 63) / 64, nqt = (s.t + 127) / 128;
+      const int ntk = (s.t + 63) / 64, nqt = (s.t + bq - 1) / bq;
       const long units = (long)nqt * ntk;
       const int lanes = attention_lanes(s.t);
       const size_t first = tl.size();
@@ -789,14 +790,14 @@ struct BarkHip {
         for (long u = units * l / lanes; u < u1;) {
           const int qi = (int)(u / ntk), kb = (int)(u % ntk);
           const int ke = (int)std::min<long>(ntk, kb + (u1 - u));
-          tl.push_back(make_int4(s.start, s.t, qi * 128, kb | (ke << 16)));
+          tl.push_back(make_int4(s.start, s.t, qi * bq, kb | (ke << 16)));
           u += ke - kb;
         }
       }
       for (size_t i = first; i < tl.size();) {
         size_t j = i + 1;
         while (j < tl.size() && tl[j].z == tl[i].z) ++j;
-        if (j - i > 1) ml.push_back(make_int4((int)i, (int)(j - i), s.start + tl[i].z, std::min(128, s.t - tl[i].z)));
+        if (j - i > 1) ml.push_back(make_int4((int)i, (int)(j - i), s.start + tl[i].z, std::min(bq, s.t - tl[i].z)));
         i = j;
       }
     }
@@ -977,11 +978,11 @@ struct BarkHip {
       AttnArgs aa{qu.as<half>(), qv.as<half>(), kh.as<half>(), vt.as<half>(),
                   rk.as<half>() + (size_t)l * HEADS * pp * HDIM,
                   ao.as<half>(), mp, pp, tc, tiles.as<int4>(), ntiles, attn_lanes.as<int>(), nlanes,
-                  attn_po.as<float>(), attn_pml.as<float>(), merges.as<int4>(), nmerges};
+                  attn_po.as<half>(), attn_pml.as<float>(), merges.as<int4>(), nmerges};
       prof.run("rel_attention", attn_flops, 2.0 * mr * HIDDEN * 5 + 2.0 * prows * HIDDEN, st,
                [&] { rel_attention(aa, st); });
       if (nmerges)  // partial (o, max, sum) of every split query tile -> heads-flat f16
-        prof.run("attn_merge", 0, (double)nparts * HEADS * 128 * (HDIM + 2) * 4 + 2.0 * mr * HIDDEN, st,
+        prof.run("attn_merge", 0, (double)nparts * HEADS * attention_query_tile() * (HDIM * 2 + 8) + 2.0 * mr * HIDDEN, st,
                  [&] { rel_attention_merge(aa, st); });
       res = resid_op("attn_out_resid", ao.as<half>(), HIDDEN, mp, mr, L.o, 1.0f, st);
       // ---- conv module

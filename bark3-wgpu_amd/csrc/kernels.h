@@ -112,8 +112,8 @@ struct AttnArgs {
   int ntiles;
   const int* lanes;   // nlanes + 1 segment offsets
   int nlanes;
-  float* part_o = nullptr;   // [slot][head][128 q][128 d]
-  float* part_ml = nullptr;  // [slot][head][128 q][2] (max, sum)
+  half* part_o = nullptr;    // [slot][head][query tile][128 d]: o / sum, f16
+  float* part_ml = nullptr;  // [slot][head][query tile][2] (max, sum)
   const int4* merges = nullptr;
   int nmerges = 0;
 };
@@ -121,6 +121,9 @@ struct AttnArgs {
 // only, so a sequence's arithmetic does not depend on the rest of its batch):
 // its query tile x key tile units are spread evenly over the lanes.
 int attention_lanes(int t);
+// Queries per attention work tile (256; 128 with BARK_HIP_ATTN_WAVES=4): the
+// unit of the tiles, merges and partial buffers of AttnArgs.
+int attention_query_tile();
 // q+u and q+v must be pre-multiplied by attention_q_scale() = log2(e)/sqrt(128)
 // (the Qkv epilogue does it when EpiArgs::scale is set to this value).
 // rel_attention writes the complete query tiles and the partials of split

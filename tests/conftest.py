@@ -18,6 +18,13 @@ def load_pkg():
     name = "bark3_wgpu_amd"
     if name in sys.modules:
         return sys.modules[name]
+    # torch ships its own HIP runtime under the same soname as ROCm's. Whichever
+    # loads first serves the process; torch only finds the GPU on its own copy,
+    # so it is imported before the library pulls in ROCm's.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     init = ROOT / "bark3-wgpu_amd" / "__init__.py"
     spec = importlib.util.spec_from_file_location(name, init, submodule_search_locations=[str(init.parent)])
     mod = importlib.util.module_from_spec(spec)
