@@ -1261,6 +1261,185 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const float* part, in
   }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny kernel: the isolated 4-bit linear at M <= 256 (short utterances),
+// where streaming the weights is the whole cost. The output is computed
+// transposed, C^T = W . A^T, so the weights are the MFMA's row operand: a
+// lane's 16-byte code load is 32 consecutive k of one output column, expanded
+// in registers into four 8-k fragments (MFMA k slots may hold any k, as long
+// as both operands agree: step c of a 64-k chunk takes k + 8c .. + 7 in lane
+// half 0 and k + 32 + 8c .. + 7 in lane half 1).
+//
+// A workgroup owns 32 output columns and 32 * MB rows; its four waves take
+// one quarter of K each and are summed through LDS in wave order (a fixed
+// order: results do not depend on timing). Each wave stages its activation
+// chunk (32 * MB rows x 64 k) through its own LDS region: loaded row by row
+// (eight rows of 128 bytes per load instruction, where fragment-shaped loads
+// touch 32-64 cache lines each and ran at the vector L1's line rate),
+// converted from bf16 on the way when needed, and read back as MFMA
+// fragments. The next chunk's codes and activations are in flight meanwhile.
+// Rows are split over workgroups, never K, so no partial sums leave the
+// workgroup (a K split finished by the last-arriving workgroup needed an
+// agent-scope release per workgroup, an L2 write-back that cost more than
+// the split saved).
+constexpr int SK_LD = 72;  // halves per staged activation row (64 used; 144 bytes)
+
+struct SkinnyArgs {
+  GemmParams p;
+  void* out;
+  int out_kind;  // 0 f32, 1 f16, 2 bf16
+};
+
+__device__ inline half8 bf16x8_to_f16(uint4 x) {  // exact for |x| in the f16 normal range
+  const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
+  half8 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[2 * e] = (half)__uint_as_float(w4[e] << 16);
+    v[2 * e + 1] = (half)__uint_as_float(w4[e] & 0xffff0000u);
+  }
+  return v;
+}
+
+// rows m, columns n .. n + 3 of C from one lane's four accumulators
+__device__ inline void skinny_store4(const SkinnyArgs& s, int m, int n, floatx4 v) {
+  const size_t o = (size_t)m * s.p.N + n;
+  if (s.out_kind == 0) {
+    *reinterpret_cast<floatx4*>(static_cast<float*>(s.out) + o) = v;
+  } else if (s.out_kind == 1) {
+    const half4 h = {to_f16(v[0]), to_f16(v[1]), to_f16(v[2]), to_f16(v[3])};
+    *reinterpret_cast<half4*>(static_cast<half*>(s.out) + o) = h;
+  } else {
+    uint32_t b[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t u = __float_as_uint(v[e]);
+      u += 0x7fffu + ((u >> 16) & 1u);  // round to nearest even (finite inputs)
+      b[e] = u >> 16;
+    }
+    *reinterpret_cast<uint2*>(static_cast<uint16_t*>(s.out) + o) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+  }
+}
+
+template <int MB, bool ABF16>
+__global__ void __launch_bounds__(256, 2) gemm_skinny_kernel(SkinnyArgs s) {
+  constexpr int ROWS = 32 * MB;
+  constexpr int LD_PER = ROWS / 8;  // row loads per lane per chunk (eight rows of 128 B per wave load)
+  __shared__ __attribute__((aligned(16))) half stage[4][ROWS * SK_LD];
+  floatx4* red = reinterpret_cast<floatx4*>(&stage[0][0]);  // [wave][row block][quad][lane], after the loop
+  static_assert(sizeof(stage) >= 4 * MB * 4 * 64 * sizeof(floatx4), "reduction fits the staging area");
+  const GemmParams& p = s.p;
+  const int n0 = blockIdx.x * 32, m0 = blockIdx.y * ROWS;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const int kq = p.K / 4, kw0 = w * kq;
+  const int n = n0 + l32;
+  const RowLut lut = load_row_lut(p.lut + (size_t)n * 16);
+  const uint8_t* crow = p.codes + (size_t)n * (p.K / 2) + 16 * lhi;
+  // staging loads: lane reads row (8 i + lane / 8), bytes 16 (lane % 8) .. + 15 of the chunk
+  const int sr = lane >> 3, sc = (lane & 7) * 8;
+  const half* abase[LD_PER];
+#pragma unroll
+  for (int i = 0; i < LD_PER; ++i)  // rows >= M read row M - 1 and are not stored
+    abase[i] = p.A + (size_t)min(m0 + 8 * i + sr, p.M - 1) * p.lda + sc;
+  int nld = 0;  // row loads that hit rows < M (uniform)
+#pragma unroll
+  for (int i = 0; i < LD_PER; ++i) nld += m0 + 8 * i < p.M;
+  half* const st = stage[w];
+
+  floatx16 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[mb][v] = 0.0f;
+  uint4 cw = *reinterpret_cast<const uint4*>(crow + kw0 / 2);
+  uint4 ar[LD_PER] = {};  // rows past the end stay zero
+  auto load_a = [&](int kc) {
+#pragma unroll
+    for (int i = 0; i < LD_PER; ++i)
+      if (i < nld) ar[i] = *reinterpret_cast<const uint4*>(abase[i] + kc);
+  };
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  load_a(kw0);
+  for (int kc = kw0; kc < kw0 + kq; kc += 64) {
+    wave_sync();  // the previous chunk's fragment reads are done
+#pragma unroll
+    for (int i = 0; i < LD_PER; ++i) {
+      const half8 v = ABF16 ? bf16x8_to_f16(ar[i]) : __builtin_bit_cast(half8, ar[i]);
+      st_half8(st + (8 * i + sr) * SK_LD + sc, v);
+    }
+    const uint32_t words[4] = {cw.x, cw.y, cw.z, cw.w};
+    if (kc + 64 < kw0 + kq) {  // uniform: the next chunk in flight
+      cw = *reinterpret_cast<const uint4*>(crow + (kc + 64) / 2);
+      load_a(kc + 64);
+    }
+    half8 wf[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) wf[c] = __builtin_bit_cast(half8, expand8<false>(words[c], lut));
+    wave_sync();  // the staged rows are visible to the whole wave
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      if (m0 + 32 * mb < p.M)  // uniform: row blocks past the end
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const half8 af = ld_half8(st + (32 * mb + l32) * SK_LD + 32 * lhi + 8 * c);
+          acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[c], af, acc[mb], 0, 0, 0);
+        }
+    }
+  }
+
+  // the four K quarters, summed in wave order; wave w finishes row block w
+  __syncthreads();  // every wave is done with its staging area
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      red[((w * MB + mb) * 4 + g) * 64 + lane] =
+          floatx4{acc[mb][4 * g], acc[mb][4 * g + 1], acc[mb][4 * g + 2], acc[mb][4 * g + 3]};
+  __syncthreads();
+  const int mb = w;
+  const int m = m0 + 32 * mb + l32;
+  if (mb >= MB || m >= p.M) return;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    floatx4 x = red[((0 * MB + mb) * 4 + g) * 64 + lane];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) {
+      const floatx4 y = red[((q * MB + mb) * 4 + g) * 64 + lane];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] += y[e];
+    }
+    skinny_store4(s, m, n0 + 8 * g + 4 * lhi, x);
+  }
+}
+
+// Skinny-kernel rows per workgroup (MB row blocks of 32): one block, which
+// gives the most workgroups (6 x N / 32 at T = 188) and measured fastest on
+// MI355X for all three config-1 shapes (a sweep of 1-4 blocks: 9.3 / 13.7 /
+// 8.7 us at MB = 1 against 9.8 / 23.6 / 9.3 at MB = 3, T = 188; each phase is
+// latency-bound, so more resident workgroups win over less code expansion).
+// BARK_HIP_SKINNY_MB = 1..4 forces a count. 0 when the kernel does not apply.
+int skinny_mb(int M, int N, int K) {
+  if (M < 1 || M > 256 || N % 32 != 0 || K % 256 != 0) return 0;
+  static const int forced = [] {
+    const char* e = getenv("BARK_HIP_SKINNY_MB");
+    return e ? atoi(e) : 0;
+  }();
+  return forced >= 1 && forced <= 4 ? forced : 1;
+}
+
+template <int MB>
+void launch_skinny_mb(const SkinnyArgs& a, bool abf16, hipStream_t st) {
+  const dim3 grid(a.p.N / 32, ceil_div(a.p.M, 32 * MB)), block(256);
+  if (abf16) BARK_LAUNCH((gemm_skinny_kernel<MB, true>), grid, block, 0, st, a);
+  else BARK_LAUNCH((gemm_skinny_kernel<MB, false>), grid, block, 0, st, a);
+}
+
 // Weight format: 0 = f16, 1 = swizzled 4-bit (encoder), 2 = plain 4-bit
 // (isolated linear; f16 or bf16 activations). Only the combinations the
 // encoder and the isolated linear use are instantiated; wide_supported()
@@ -1699,9 +1878,35 @@ int isolated_splits(int M, const GemmWeight& W) {
 
 // The isolated linear with its partial sums in `part` (bytes available:
 // part_bytes), or in the grow-only per-stream workspace when part is null.
+// The skinny kernel for M <= 256 (plain 4-bit weights), else the wide
+// kernels, with K split into partial sums in `part` (bytes available:
+// part_bytes), or in the grow-only per-stream workspace when part is null,
+// and one pass adding them in order.
 void isolated_with(const half* A, int M, const GemmWeight& W, void* C, int c_kind, hipStream_t stream,
                    bool a_bf16, float* part, size_t part_bytes) {
   BARK_REQUIRE(c_kind >= 0 && c_kind <= 2, "gemm_isolated: bad output kind");
+  const int mb = W.lut4() && !W.swizzled ? skinny_mb(M, W.n, W.k) : 0;
+  if (mb > 0) {
+    BARK_REQUIRE(A != nullptr && W.lut != nullptr && C != nullptr, "gemm_isolated: null operand");
+    BARK_REQUIRE((size_t)W.n * W.k / 2 < (1ull << 31) && (size_t)M * W.k < (1ull << 31),
+                 "gemm_isolated: operand too large");
+    SkinnyArgs a;
+    a.p.A = A;
+    a.p.lda = W.k;
+    a.p.codes = W.codes;
+    a.p.lut = W.lut;
+    a.p.M = M;
+    a.p.N = W.n;
+    a.p.K = W.k;
+    a.out = C;
+    a.out_kind = c_kind;
+    if (mb == 1) launch_skinny_mb<1>(a, a_bf16, stream);
+    else if (mb == 2) launch_skinny_mb<2>(a, a_bf16, stream);
+    else if (mb == 3) launch_skinny_mb<3>(a, a_bf16, stream);
+    else launch_skinny_mb<4>(a, a_bf16, stream);
+    BARK_HIP_CHECK(hipGetLastError());
+    return;
+  }
   const int splits = isolated_splits(M, W);
   if (splits == 1) {
     EpiArgs e;
