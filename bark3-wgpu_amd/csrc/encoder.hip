@@ -236,6 +236,16 @@ struct BarkHip {
   std::vector<void*> allocs;  // weights, freed at destroy
   Profiler prof;
   std::vector<int> table_key;  // plan whose row bounds / query tiles are on the device
+  // The encode (front end + blocks) as a HIP graph, for short utterances
+  // where launching ~370 kernels one by one costs more than running them.
+  // Keyed on the packing, the input pointer and ws_gen (bumped by every
+  // workspace reallocation, so no baked-in pointer goes stale): the first call
+  // with a key runs eagerly, a repeat captures it on cap_stream, later repeats
+  // replay it. BARK_HIP_GRAPH=0 turns it off; profiling runs eagerly.
+  long ws_gen = 0;
+  hipStream_t cap_stream = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  std::vector<long> graph_key, last_key;
   GemmWeight sub_w, proj_w, sub_pw1, sub_pw2;
   // relative_k_proj of every layer stacked (row block l = layer l): the
   // position keys depend on T only, so all layers' relK come from one GEMM.
@@ -338,6 +348,7 @@ struct BarkHip {
     b.cap = 0;
     const size_t want = (bytes + 4095) & ~size_t(4095);
     BARK_HIP_CHECK(hipMalloc(&b.p, want));
+    ++ws_gen;
     BARK_HIP_CHECK(hipMemset(b.p, 0, want));
     // the fill runs on the null stream, which the library's non-blocking
     // streams do not wait for: finish it before anything is queued after it
@@ -355,6 +366,8 @@ struct BarkHip {
                       &tdt_c, &tdt_dec, &tdt_part, &tdt_tokens, &tdt_pooler, &tdt_params};
     for (DevBuf* b : bufs)
       if (b->p) (void)hipFree(b->p);
+    if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+    if (cap_stream) (void)hipStreamDestroy(cap_stream);
     if (stream) (void)hipStreamDestroy(stream);
     if (done) (void)hipEventDestroy(done);
     if (tables_copied) (void)hipEventDestroy(tables_copied);
@@ -1034,6 +1047,49 @@ struct BarkHip {
   // written to out + (sum of earlier t) * 640 with `kind` host or device.
   // out == nullptr leaves the poolers in the workspace (sequence i at row
   // rows_out[i].first, rows_out[i].second rows) for a decode that follows.
+  // body(stream) queues one encode; see graph_exec for when it is captured.
+  template <class F>
+  void run_graphed(const std::vector<long>& key, F&& body, hipStream_t st) {
+    static const bool enabled = [] {
+      const char* e = getenv("BARK_HIP_GRAPH");
+      return !(e && atoi(e) == 0);
+    }();
+    if (!enabled || prof.on) {
+      body(st);
+      return;
+    }
+    if (graph_exec && key == graph_key) {
+      BARK_HIP_CHECK(hipGraphLaunch(graph_exec, st));
+      return;
+    }
+    if (key != last_key) {  // a new packing: eager (most are never repeated)
+      last_key = key;
+      body(st);
+      return;
+    }
+    if (!cap_stream) BARK_HIP_CHECK(hipStreamCreateWithFlags(&cap_stream, hipStreamNonBlocking));
+    if (graph_exec) {
+      BARK_HIP_CHECK(hipGraphExecDestroy(graph_exec));
+      graph_exec = nullptr;
+      graph_key.clear();
+    }
+    hipGraph_t g = nullptr;
+    BARK_HIP_CHECK(hipStreamBeginCapture(cap_stream, hipStreamCaptureModeThreadLocal));
+    try {
+      body(cap_stream);
+    } catch (...) {
+      (void)hipStreamEndCapture(cap_stream, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    BARK_HIP_CHECK(hipStreamEndCapture(cap_stream, &g));
+    const hipError_t e = hipGraphInstantiate(&graph_exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    BARK_HIP_CHECK(e);
+    graph_key = key;
+    BARK_HIP_CHECK(hipGraphLaunch(graph_exec, st));
+  }
+
   void encode_mel_batch(const float* mel_in, bool mel_on_device, const int32_t* frames,
                         const int32_t* valid, int batch, int32_t* t_out, float* out,
                         bool out_on_device, size_t cap, hipStream_t st,
@@ -1057,13 +1113,18 @@ struct BarkHip {
       dmel = mel.as<float>();
     }
     upload_tables(pl, st);
-    BARK_HIP_CHECK(hipMemsetAsync(sub16.p, 0, (size_t)pl.mp * 4096 * 2, st));
-    size_t foff = 0;
-    for (const auto& s : pl.seqs) {
-      front_end(dmel + foff * MEL, s, st);
-      foff += s.frames;
-    }
-    encoder_blocks(pl, -1, st);
+    auto body = [&](hipStream_t s_) {
+      zero_fill(sub16.p, (size_t)pl.mp * 4096 * 2, s_);
+      size_t foff = 0;
+      for (const auto& s : pl.seqs) {
+        front_end(dmel + foff * MEL, s, s_);
+        foff += s.frames;
+      }
+      encoder_blocks(pl, -1, s_);
+    };
+    std::vector<long> key{pl.mp, pl.tc, (long)reinterpret_cast<uintptr_t>(dmel), ws_gen};
+    for (const auto& s : pl.seqs) key.insert(key.end(), {s.frames, s.valid, s.t, s.start});
+    run_graphed(key, body, st);
     size_t orow = 0;
     if (rows_out) rows_out->clear();
     for (size_t i = 0; i < pl.seqs.size(); ++i) {
@@ -1159,7 +1220,7 @@ struct BarkHip {
     BARK_HIP_CHECK(hipMemcpyAsync(subf32.p, sub_rows, (size_t)t * 4096 * 4,
                                   hipMemcpyHostToDevice, st));
     upload_tables(pl, st);
-    BARK_HIP_CHECK(hipMemsetAsync(sub16.p, 0, (size_t)pl.mp * 4096 * 2, st));
+    zero_fill(sub16.p, (size_t)pl.mp * 4096 * 2, st);
     f32_to_f16_rows(subf32.as<float>(), t, 4096, sub16.as<half>(), 4096, st);
     encoder_blocks(pl, dump_layer, st);
     if (out_pooler)

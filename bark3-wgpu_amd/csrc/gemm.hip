@@ -532,8 +532,11 @@ __device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p
   else epilogue(std::integral_constant<bool, true>());
 }
 
-// Wide-tile kernel: workgroup tile (32*FM) x 256, the four waves side by
-// side, each owning all rows and 64 columns (FM x 2 MFMA blocks). B never
+// Wide-tile kernel: workgroup tile (32*FM) x 64*WV, the WV waves (4, or 1
+// for short inputs, where 4-wave tiles would leave most CUs idle) side by
+// side, each owning all rows and 64 columns (FM x 2 MFMA blocks). Every output
+// element is one MFMA chain over its k in the same order whatever FM and WV
+// are, so the tile shape never changes results. B never
 // touches LDS: an MFMA B fragment is 8 consecutive k of one weight row, i.e.
 // one u32 of 4-bit codes (expanded in registers with the lane's two row
 // tables) or 16 bytes of f16 weights. Only A is staged through LDS. The k
@@ -543,10 +546,14 @@ __device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p
 // formats therefore accumulate in the same order and give bit-identical
 // results for the same weight values. Per k-tile a wave runs 8*FM MFMAs
 // against 4*FM fragment reads (and 8 code expansions in 4-bit mode).
-template <int FM, bool LUT4, bool SWZ, bool ABF16, int EPI>
-__global__ void __launch_bounds__(256, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kernel(GemmParams p) {
+// K2ORD: accumulate slices 0-1 and 2-3 of every k-tile in two chains and add
+// them at the end, the two-group kernel's order (used for its epilogues, so
+// the tile shape still never changes results).
+template <int FM, bool LUT4, bool SWZ, bool ABF16, int EPI, int WV = 4, bool K2ORD = false>
+__global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kernel(GemmParams p) {
+  constexpr int NT = 64 * WV;  // threads: WV waves of 64 columns each
   constexpr int BM = 32 * FM;
-  constexpr int A_CH = BM * BK / 8 / 256;  // 16-byte chunks of A per thread per k-tile (= FM)
+  constexpr int A_CH = BM * BK / 8 / NT;  // 16-byte chunks of A per thread per k-tile
   constexpr int B_V = LUT4 ? 2 : 8;        // 16-byte loads of B per lane per k-tile
   // 4-bit tiles of up to 128 rows keep two workgroups per CU (two waves per
   // SIMD, so one wave's code expansion overlaps the other's MFMAs): that needs
@@ -569,7 +576,7 @@ __global__ void __launch_bounds__(256, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kern
   const int xq = G / 8, xr = G % 8, xcd = bid % 8;
   const int tix = xcd * xq + min(xcd, xr) + bid / 8;
   const int bz = tix / (gx * gy), by = (tix / gx) % gy, bx = tix % gx;
-  const int n0 = bx * 256, m0 = by * BM;
+  const int n0 = bx * NT, m0 = by * BM;
   const int nw = n0 + wid * 64;
   // K chunk of this split: whole 256-k units, the first K/256 % splits
   // chunks one unit longer (depends on K and the split count only)
@@ -595,7 +602,7 @@ __global__ void __launch_bounds__(256, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kern
   int a_lds[A_CH];
 #pragma unroll
   for (int i = 0; i < A_CH; ++i) {
-    const int ch = tid + 256 * i, row = ch >> 3, col = (ch & 7) * 8;
+    const int ch = tid + NT * i, row = ch >> 3, col = (ch & 7) * 8;
     aoff[i] = (uint32_t)min(row, p.M - 1 - m0) * (uint32_t)p.lda + col;  // rows past M repeat row M-1
     a_lds[i] = row * LDK + col;
   }
@@ -643,13 +650,20 @@ __global__ void __launch_bounds__(256, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kern
     }
   };
 
-  floatx16 acc[FM][2];
+  floatx16 acc[FM][2], acc_hi[K2ORD ? FM : 1][2];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  if constexpr (K2ORD)
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc_hi[i][j][v] = 0.0f;
 
   // A fragment row offset of block i for this lane, k slice s: chunk 4*lhi + s.
   const int af_off = l32 * LDK + 32 * lhi;
@@ -711,8 +725,13 @@ __global__ void __launch_bounds__(256, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kern
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) {
+          if (K2ORD && s >= 2)
+            acc_hi[K2ORD ? i : 0][j] =
+                __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc_hi[K2ORD ? i : 0][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
+        }
 #pragma unroll
       for (int m = 0; m < 2 * FM; ++m) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -749,6 +768,13 @@ __global__ void __launch_bounds__(256, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kern
     tile(1, 0, BD == 4 ? rb3 : rb1, ra0, kt + 3 + AD, AD == 4 ? ra3 : ra1, kt + 3 + BD, BD == 4 ? rb3 : rb1);
     __syncthreads();
   }
+  if constexpr (K2ORD)
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] += acc_hi[i][j][v];
 
   tile_epilogue<FM, EPI>(acc, p, m0, nw, bz, lane);
 }
@@ -1461,11 +1487,17 @@ bool wide_supported(Epi epi, int fmt) {
   }
 }
 
-template <int FM>
+template <int FM, int WV = 4, bool K2ORD = false>
 void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t s) {
-  dim3 grid(p.N / 256, ceil_div(p.M, 32 * FM), p.splits), block(256);
+  dim3 grid(p.N / (64 * WV), ceil_div(p.M, 32 * FM), p.splits), block(64 * WV);
+  if constexpr (K2ORD) {  // the two-group kernel's default epilogue only
+    BARK_REQUIRE(epi == Epi::Silu && fmt != 2, "gemm: no two-group-order wide kernel for this epilogue");
+    if (fmt == 0) BARK_LAUNCH((gemm_wide_kernel<FM, false, false, false, (int)Epi::Silu, WV, true>), grid, block, 0, s, p);
+    else BARK_LAUNCH((gemm_wide_kernel<FM, true, true, false, (int)Epi::Silu, WV, true>), grid, block, 0, s, p);
+    return;
+  }
 #define BARK_K(L4, SW, AB, E) \
-  BARK_LAUNCH((gemm_wide_kernel<FM, L4, SW, AB, (int)Epi::E>), grid, block, 0, s, p)
+  BARK_LAUNCH((gemm_wide_kernel<FM, L4, SW, AB, (int)Epi::E, WV>), grid, block, 0, s, p)
 #define BARK_CASE(E)                                   \
   case Epi::E:                                         \
     if (fmt == 0) BARK_K(false, false, false, E);      \
@@ -1704,6 +1736,38 @@ int pick_wide_fm(int M, int N, int K, int splits = 1) {
   return best;
 }
 
+// Short inputs (a few row tiles): one-wave workgroups of 32 or 64 rows x 64
+// columns, which give 4x the workgroups of the four-wave tiles. Chosen when
+// the four-wave tiles of 64 rows would fill fewer than half the CUs; the
+// height is the one with more workgroups unless they would exceed four per
+// CU. Returns 0 (use the four-wave tiles) or the height in row blocks (1, 2).
+// BARK_HIP_GEMM_NARROW = 0/1/2 forces it off or a height.
+int pick_narrow_fm(int M, int N, int splits) {
+  static const int forced = [] {
+    const char* e = getenv("BARK_HIP_GEMM_NARROW");
+    return e ? atoi(e) : -1;
+  }();
+  if (forced >= 0 && forced <= 2) return forced;
+  if (N % 64 != 0) return 0;
+  const long wide_tiles = (long)ceil_div(M, 64) * (N / 256) * splits;
+  if (wide_tiles >= 128) return 0;
+  return (long)ceil_div(M, 32) * (N / 64) * splits <= 1024 ? 1 : 2;
+}
+
+void launch_fm(int fm, int narrow, const GemmParams& p, Epi epi, int fmt, bool a_bf16, hipStream_t stream,
+               bool k2ord = false) {
+  if (narrow == 1 && k2ord) launch_wide<1, 1, true>(p, epi, fmt, a_bf16, stream);
+  else if (narrow == 2 && k2ord) launch_wide<2, 1, true>(p, epi, fmt, a_bf16, stream);
+  else if (narrow == 1) launch_wide<1, 1>(p, epi, fmt, a_bf16, stream);
+  else if (narrow == 2) launch_wide<2, 1>(p, epi, fmt, a_bf16, stream);
+  else if (fm == 8) launch_wide<8>(p, epi, fmt, a_bf16, stream);
+  else if (fm == 6) launch_wide<6>(p, epi, fmt, a_bf16, stream);
+  else if (fm == 5) launch_wide<5>(p, epi, fmt, a_bf16, stream);
+  else if (fm == 4) launch_wide<4>(p, epi, fmt, a_bf16, stream);
+  else if (fm == 3) launch_wide<3>(p, epi, fmt, a_bf16, stream);
+  else launch_wide<2>(p, epi, fmt, a_bf16, stream);
+}
+
 }  // namespace
 
 void swizzle_codes(uint8_t* codes, size_t nbytes) {
@@ -1730,7 +1794,18 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   BARK_REQUIRE(!a_bf16 || (W.lut4() && !W.swizzled), "gemm: bf16 activations need plain 4-bit weights");
   const bool fits32 = (double)M * lda * 2 < 4.0e9 && (double)W.n * W.k * 2 < 4.0e9;
   const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
-  if (W.n % 256 == 0 && fits32 && W.k / BK >= 4 && k2_supported(epi, fmt) && k2_default(epi)) {
+  // short inputs: one-wave tiles, in the two-group kernel's summation order
+  // where that kernel is the default (Silu), so results match longer inputs
+  const bool k2 = W.n % 256 == 0 && fits32 && W.k / BK >= 4 && k2_supported(epi, fmt) && k2_default(epi);
+  const int narrow = W.n % 256 == 0 && fits32 && wide_supported(epi, fmt) && (!k2 || epi == Epi::Silu)
+                         ? pick_narrow_fm(M, W.n, 1)
+                         : 0;
+  if (narrow) {
+    launch_fm(0, narrow, p, epi, fmt, a_bf16, stream, k2);
+    BARK_HIP_CHECK(hipGetLastError());
+    return;
+  }
+  if (k2) {
     const int fm2 = pick_k2_fm(M, W.n, 1);
     if (fm2) {
       launch_k2_fm(fm2, p, epi, fmt, a_bf16, stream);
@@ -1740,12 +1815,7 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   }
   const int fm = W.n % 256 == 0 && fits32 && wide_supported(epi, fmt) ? pick_wide_fm(M, W.n, W.k) : 0;
   if (fm) {
-    if (fm == 8) launch_wide<8>(p, epi, fmt, a_bf16, stream);
-    else if (fm == 6) launch_wide<6>(p, epi, fmt, a_bf16, stream);
-    else if (fm == 5) launch_wide<5>(p, epi, fmt, a_bf16, stream);
-    else if (fm == 4) launch_wide<4>(p, epi, fmt, a_bf16, stream);
-    else if (fm == 3) launch_wide<3>(p, epi, fmt, a_bf16, stream);
-    else launch_wide<2>(p, epi, fmt, a_bf16, stream);
+    launch_fm(fm, 0, p, epi, fmt, a_bf16, stream);
     BARK_HIP_CHECK(hipGetLastError());
     return;
   }
@@ -1774,6 +1844,7 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
   ea.ldo = ldo;
   GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, splits, (size_t)M * ldo};
   const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
+  const int narrow = k2_default(Epi::StoreF32) ? 0 : pick_narrow_fm(M, W.n, splits);
   if (k2_default(Epi::StoreF32)) {
     const int fm2 = pick_k2_fm(M, W.n, splits);
     if (fm2) {
@@ -1784,12 +1855,7 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
   }
   int fm = pick_wide_fm(M, W.n, W.k, splits);
   if (fm == 0) fm = 2;
-  if (fm == 8) launch_wide<8>(p, Epi::StoreF32, fmt, a_bf16, stream);
-  else if (fm == 6) launch_wide<6>(p, Epi::StoreF32, fmt, a_bf16, stream);
-  else if (fm == 5) launch_wide<5>(p, Epi::StoreF32, fmt, a_bf16, stream);
-  else if (fm == 4) launch_wide<4>(p, Epi::StoreF32, fmt, a_bf16, stream);
-  else if (fm == 3) launch_wide<3>(p, Epi::StoreF32, fmt, a_bf16, stream);
-  else launch_wide<2>(p, Epi::StoreF32, fmt, a_bf16, stream);
+  launch_fm(fm, narrow, p, Epi::StoreF32, fmt, a_bf16, stream);
   BARK_HIP_CHECK(hipGetLastError());
 }
 

@@ -150,6 +150,9 @@ void apply_residual(float* x, int rows, const ResidIn& res, hipStream_t stream);
 void dwconv_bn_silu(const float* g, const float* dw, const float* bn_a, const float* bn_b,
                     const int2* bounds, half* out, int rows, hipStream_t stream);
 void f32_to_f16(const float* x, half* y, size_t n, hipStream_t stream);
+// p[0 .. bytes) = 0 with a kernel (no memset node when captured in a graph);
+// bytes and p in 16-byte units.
+void zero_fill(void* p, size_t bytes, hipStream_t stream);
 void f32_to_f16_rows(const float* x, int rows, int cols, half* y, int ldy,
                      hipStream_t stream);
 void copy_rows_f32(const float* x, int ldx, float* y, int ldy, int rows, int cols,

@@ -427,6 +427,19 @@ void dwconv_bn_silu(const float* g, const float* dw, const float* bn_a, const fl
   BARK_HIP_CHECK(hipGetLastError());
 }
 
+__global__ void __launch_bounds__(256) zero_fill_kernel(uint4* p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256) p[i] = uint4{0, 0, 0, 0};
+}
+
+void zero_fill(void* p, size_t bytes, hipStream_t stream) {
+  BARK_REQUIRE(bytes % 16 == 0 && reinterpret_cast<uintptr_t>(p) % 16 == 0, "zero_fill: 16-byte units");
+  const size_t n16 = bytes / 16;
+  if (n16 == 0) return;
+  BARK_LAUNCH(zero_fill_kernel, dim3((unsigned)std::min<size_t>((n16 + 255) / 256, 4096)), dim3(256), 0, stream,
+              static_cast<uint4*>(p), n16);
+  BARK_HIP_CHECK(hipGetLastError());
+}
+
 void f32_to_f16(const float* x, half* y, size_t n, hipStream_t stream) {
   if (n == 0) return;
   BARK_LAUNCH(f32_to_f16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,

@@ -125,6 +125,55 @@ def test_two_streams_back_to_back(pkg, synth):
     assert np.array_equal(got_a, want_a) and np.array_equal(got_b, want_b)
 
 
+def test_graph_replays_equal_eager(pkg, synth):
+    """A repeated packing replays a captured HIP graph of the encode (the first
+    call runs eagerly, the second captures). Every replay, with eager work and
+    synchronisations in between (another packing, torch kernels, the isolated
+    linear), equals the eager result bit for bit."""
+    import torch
+
+    src = synth.SynthCheckpoint(seed=46, n_layers=2, style="rich", lowbit=True)
+    fa, fb = 1500, 700
+    ma, mb = synth.mel(fa, seed=3), synth.mel(fb, seed=4)
+    ta = pkg.conv_len(pkg.conv_len(pkg.conv_len(fa)))
+    tb = pkg.conv_len(pkg.conv_len(pkg.conv_len(fb)))
+    print(f"case graph replays T={ta},{tb}", flush=True)
+    with pkg.HipEncoder.load_with(src, n_layers=2) as enc:
+        da, db = torch.from_numpy(ma).cuda(), torch.from_numpy(mb).cuda()
+        pa = torch.empty((ta, 640), device="cuda")
+        pb = torch.empty((tb, 640), device="cuda")
+        sp = torch.cuda.current_stream().cuda_stream
+
+        def run_a():
+            pa.fill_(float("nan"))
+            enc.encode_mel_batch_device(da.data_ptr(), [fa], [fa], pa.data_ptr(), pa.numel(), sp)
+            torch.cuda.synchronize()
+            return pa.cpu().numpy().copy()
+
+        def run_b():
+            pb.fill_(float("nan"))
+            enc.encode_mel_batch_device(db.data_ptr(), [fb], [fb], pb.data_ptr(), pb.numel(), sp)
+            torch.cuda.synchronize()
+            return pb.cpu().numpy().copy()
+
+        want_a = run_a()  # eager
+        want_b, _ = enc.encode_mel(mb)
+        A = torch.randn((64, 1024), device="cuda").to(torch.bfloat16)
+        codes = torch.randint(0, 256, (1024, 512), device="cuda", dtype=torch.uint8)
+        lut = torch.sort(torch.randn((1024, 16), device="cuda") * 0.02, dim=1).values.half()
+        C = torch.empty((64, 1024), device="cuda", dtype=torch.bfloat16)
+        for i in range(6):  # capture on the first repeat, replays after
+            assert np.array_equal(run_a(), want_a), f"replay {i} differs from the eager encode"
+            x = torch.randn(4096, device="cuda").cumsum(0)  # eager torch work between replays
+            pkg.lowbit_linear(A.data_ptr(), 1, codes.data_ptr(), lut.data_ptr(), C.data_ptr(), 2, 64, 1024, 1024, sp)
+            torch.cuda.synchronize()
+            assert bool(torch.isfinite(x).all())
+        # alternating packings: each call still equals its eager result
+        for i in range(4):
+            assert np.array_equal(run_b(), want_b), f"packing B, round {i}"
+            assert np.array_equal(run_a(), want_a), f"packing A after B, round {i}"
+
+
 def test_batch_equals_individual(pkg, synth):
     """configs[4] semantics: each utterance of a packed batch equals its own
     batch-1 run (identical per-row arithmetic, so the match is exact)."""
