@@ -1709,7 +1709,7 @@ void launch_plain(const GemmParams& p, Epi epi, bool abf16, hipStream_t s) {
 // Two-block tiles run two workgroups per CU once there are more than one per
 // CU. Rates and the short-K rule are from sweeps of the encoder shapes on
 // MI355X. BARK_HIP_GEMM_WIDE = 0/2/3/4/5/6/8 forces a choice.
-int pick_wide_fm(int M, int N, int K, int splits = 1) {
+int pick_wide_fm(int M, int N, int K, int splits = 1, int max_fm = 8) {
   static const int forced = [] {
     const char* e = getenv("BARK_HIP_GEMM_WIDE");
     return e ? atoi(e) : -1;
@@ -1724,6 +1724,7 @@ int pick_wide_fm(int M, int N, int K, int splits = 1) {
   const int fms[6] = {2, 3, 4, 5, 6, 8};
   const double rate[6] = {0.9, 0.95, 1.0, 1.05, 1.1, 1.15};
   for (int i = 0; i < 6; ++i) {
+    if (fms[i] > max_fm) break;
     const long tiles = (long)ceil_div(M, 32 * fms[i]) * (N / 256) * splits;
     const long slots = (fms[i] == 2 && tiles > CUS) ? 2 * CUS : CUS;
     const long rounds = (tiles + slots - 1) / slots;
@@ -1756,8 +1757,7 @@ int pick_narrow_fm(int M, int N, int splits) {
 
 void launch_fm(int fm, int narrow, const GemmParams& p, Epi epi, int fmt, bool a_bf16, hipStream_t stream,
                bool k2ord = false) {
-  if (narrow == 1 && k2ord) launch_wide<1, 1, true>(p, epi, fmt, a_bf16, stream);
-  else if (narrow == 2 && k2ord) launch_wide<2, 1, true>(p, epi, fmt, a_bf16, stream);
+  if (narrow >= 1 && k2ord) launch_wide<1, 1, true>(p, epi, fmt, a_bf16, stream);
   else if (narrow == 1) launch_wide<1, 1>(p, epi, fmt, a_bf16, stream);
   else if (narrow == 2) launch_wide<2, 1>(p, epi, fmt, a_bf16, stream);
   else if (fm == 8) launch_wide<8>(p, epi, fmt, a_bf16, stream);
@@ -1800,8 +1800,8 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   const int narrow = W.n % 256 == 0 && fits32 && wide_supported(epi, fmt) && (!k2 || epi == Epi::Silu)
                          ? pick_narrow_fm(M, W.n, 1)
                          : 0;
-  if (narrow) {
-    launch_fm(0, narrow, p, epi, fmt, a_bf16, stream, k2);
+  if (narrow) {  // the two-chain order at 64 rows spills: one row block there
+    launch_fm(0, k2 ? 1 : narrow, p, epi, fmt, a_bf16, stream, k2);
     BARK_HIP_CHECK(hipGetLastError());
     return;
   }
@@ -1813,7 +1813,10 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
       return;
     }
   }
-  const int fm = W.n % 256 == 0 && fits32 && wide_supported(epi, fmt) ? pick_wide_fm(M, W.n, W.k) : 0;
+  // the qkv epilogue spills heavily above four row blocks (0.9-1.3 KB per
+  // lane, 30-80x slower launches), so its tiles stop at 128 rows
+  const int max_fm = epi == Epi::Qkv ? 4 : 8;
+  const int fm = W.n % 256 == 0 && fits32 && wide_supported(epi, fmt) ? pick_wide_fm(M, W.n, W.k, 1, max_fm) : 0;
   if (fm) {
     launch_fm(fm, 0, p, epi, fmt, a_bf16, stream);
     BARK_HIP_CHECK(hipGetLastError());

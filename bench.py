@@ -8,8 +8,9 @@ conv front end + 24 blocks + projector over that utterance, with the mel
 already resident in HBM. value = audio seconds per second (encoder RTFx).
 
 Also reported:
-  roofline     - the dominant kernel of the step (found in a separate pass
-                 that times every launch), from HIP events attached to its
+  roofline     - the dominant kernel of the step (the largest time per step
+                 in a separate pass that times every launch), from HIP events
+                 attached to its
                  dispatches on the library's stream during the timed region
                  (every 8th launch of it, so the timing adds ~0.5 % to the
                  step);
@@ -22,6 +23,12 @@ Also reported:
                  HBM with synthetic decoder weights (ms per decode, tokens);
   pipeline_wave_to_tokens - the workload's wave from host memory through
                  log-mel, encoder and TDT decoder to tokens in one call;
+  workloads    - configs[2] (T = 188, f16 weights; and the 4-bit encoder at
+                 T = 188) with the weight-streaming HBM fraction, and
+                 configs[4] (16 utterances of U(5, 60) s in one packed call;
+                 the 20-minute T = 15000 stream with its attention roofline);
+  roofline_runner_up - the second-largest operator's roofline from the
+                 all-launch pass;
   cpu_baseline - the CPU oracle (C restatement of the reference CPU backend)
                  on this host's cores: by default the complete workload
                  (--cpu-blocks 24); fewer blocks time a sample and scale the
@@ -90,11 +97,9 @@ def bench_encoder(pkg, synth, torch, steps: int, warmup: int):
         step()
     torch.cuda.synchronize()
     prof = enc.profile_report()
-    # the dominant kernel; in the timed region only its launches carry events.
-    # Labels within 3 % of the largest share are ties, settled by the longer
-    # launch (its event timing has the smaller relative error).
-    top = max(v["ms"] for v in prof.values())
-    dom = max((k for k in prof if prof[k]["ms"] >= 0.97 * top), key=lambda k: prof[k]["ms"] / prof[k]["count"])
+    # the dominant kernel (largest time per step); in the timed region only
+    # its launches carry events
+    dom = max(prof, key=lambda k: prof[k]["ms"])
     enc.profile_only(dom)
     enc.profile(True)
     torch.cuda.synchronize()
@@ -107,8 +112,7 @@ def bench_encoder(pkg, synth, torch, steps: int, warmup: int):
     enc.profile(False)
     log(f"[bench] encoder step {dt * 1e3:.3f} ms over {steps} steps (T={T})")
     pipe = bench_pipeline(enc)
-    enc.close()
-    return dt, T, prof, dom, timed, pipe
+    return enc, dt, T, prof, dom, timed, pipe
 
 
 def bench_pipeline(enc, reps: int = 3):
@@ -161,6 +165,115 @@ def bench_gemm(pkg, torch, T: int, K: int, N: int, reps: int = 192):
     torch.cuda.empty_cache()
     return {"T": T, "K": K, "N": N, "us": t * 1e6, "tflops": F / t / 1e12, "gbs": B / t / 1e9,
             "mfma_frac": F / t / 1e12 / PEAK_F16_TFLOPS, "hbm_frac": B / t / 1e9 / PEAK_HBM_GBS}
+
+
+# Linear weights streamed by one encode: per block the FFN pair twice, qkv,
+# out, pointwise 1 and 2 and the relative-position key projection
+# (25,165,824 weights over 18,432 output rows); f16, or 4-bit codes plus a
+# 16-entry f16 table per row.
+BLOCK_WEIGHTS, BLOCK_ROWS = 25_165_824, 18_432
+
+
+def weight_bytes(lowbit: bool) -> float:
+    per = BLOCK_WEIGHTS / 2 + 32 * BLOCK_ROWS if lowbit else 2 * BLOCK_WEIGHTS
+    return 24.0 * per
+
+
+def timed_encodes(torch, step, reps: int) -> float:
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps
+
+
+def bench_t188(enc, pkg, synth, torch, lowbit: bool, reps: int = 50):
+    """configs[2] (f16 weights from a bf16 checkpoint) or its 4-bit variant:
+    the 24-block encoder on a 15 s log-mel [1500, 128] -> T = 188, batch 1,
+    mel in HBM. Repeats of one packing replay a captured HIP graph."""
+    own = enc is None
+    if own:
+        src = synth.SynthCheckpoint(seed=0, n_layers=24, style="baseline", lowbit=lowbit)
+        enc = pkg.HipEncoder.load_with(src, device=0, n_layers=24)
+    frames = 1500
+    mel = torch.from_numpy(synth.mel(frames, seed=2)).cuda()
+    T = pkg.conv_len(pkg.conv_len(pkg.conv_len(frames)))
+    out = torch.empty((T, 640), device="cuda")
+    sp = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        enc.encode_mel_batch_device(mel.data_ptr(), [frames], [frames], out.data_ptr(), out.numel(), sp)
+
+    for _ in range(5):
+        step()
+    dt = timed_encodes(torch, step, reps)
+    assert bool(torch.isfinite(out).all()), "non-finite encoder output"
+    if own:
+        enc.close()
+    wb = weight_bytes(lowbit)
+    return {"workload": ("BASELINE configs[2]: 24-block encoder, f16 weights (bf16 checkpoint), log-mel 1500x128 -> T=188"
+                         if not lowbit else "configs[2] input through the 4-bit encoder of configs[3], T=188"),
+            "T": T, "ms_per_encode": dt * 1e3, "audio_s_per_s": frames * 0.01 / dt, "reps": reps,
+            "weight_bytes": wb, "weight_gbs": wb / dt / 1e9, "hbm_frac": wb / dt / 1e9 / PEAK_HBM_GBS}
+
+
+def bench_batch16(enc, pkg, synth, torch, reps: int = 5):
+    """16 utterances with lengths drawn uniformly from 5-60 s
+    (seeded), packed into one batched encode (per-sequence masks in attention
+    and the depthwise conv), mel in HBM."""
+    rng = np.random.default_rng(4)
+    secs = rng.uniform(5.0, 60.0, 16)
+    frames = [int(round(x * 100)) for x in secs]
+    mel = torch.from_numpy(np.concatenate([synth.mel(f, seed=100 + i) for i, f in enumerate(frames)])).cuda()
+    ts = [pkg.conv_len(pkg.conv_len(pkg.conv_len(f))) for f in frames]
+    out = torch.empty((sum(ts), 640), device="cuda")
+    sp = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        enc.encode_mel_batch_device(mel.data_ptr(), frames, frames, out.data_ptr(), out.numel(), sp)
+
+    for _ in range(2):
+        step()
+    dt = timed_encodes(torch, step, reps)
+    assert bool(torch.isfinite(out).all()), "non-finite encoder output"
+    audio = sum(frames) * 0.01
+    return {"workload": "BASELINE configs[4] batch: 16 utterances U(5,60) s (seed 4), 24-block 4-bit encoder, one packed call",
+            "audio_s": audio, "frames": sum(frames), "T_total": sum(ts), "T_max": max(ts), "ms_per_batch": dt * 1e3,
+            "audio_s_per_s": audio / dt, "reps": reps}
+
+
+def bench_long_stream(enc, pkg, synth, torch, reps: int = 3):
+    """configs[4] single stream: 20 minutes (log-mel [120000, 128]) -> T = 15000
+    through the 24-block 4-bit encoder as one sequence; with the attention
+    kernel's roofline from HIP events on its launches."""
+    frames = 120000
+    mel = torch.from_numpy(synth.mel(frames, seed=5)).cuda()
+    T = pkg.conv_len(pkg.conv_len(pkg.conv_len(frames)))
+    out = torch.empty((T, 640), device="cuda")
+    sp = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        enc.encode_mel_batch_device(mel.data_ptr(), [frames], [frames], out.data_ptr(), out.numel(), sp)
+
+    step()
+    dt = timed_encodes(torch, step, reps)
+    assert bool(torch.isfinite(out).all()), "non-finite encoder output"
+    enc.profile_only("rel_attention")
+    enc.profile(True)
+    step()
+    torch.cuda.synchronize()
+    a = enc.profile_report()["rel_attention"]
+    enc.profile(False)
+    enc.profile_only(None)
+    avg = a["ms"] / a["count"] / 1e3
+    tf = 6144.0 * T * T / avg / 1e12
+    del mel, out
+    torch.cuda.empty_cache()
+    return {"workload": "BASELINE configs[4] stream: 20 min log-mel 120000x128 -> T=15000, 24-block 4-bit encoder",
+            "T": T, "ms_per_encode": dt * 1e3, "audio_s_per_s": frames * 0.01 / dt, "reps": reps,
+            "attention": {"avg_launch_us": avg * 1e6, "tflops": tf, "frac": tf / PEAK_F16_TFLOPS,
+                          "flops_per_launch": 6144.0 * T * T}}
 
 
 def mel_wave() -> "np.ndarray":
@@ -295,7 +408,29 @@ def cpu_baseline(synth, blocks: int):
         total = t_front + t_lin + 24 * t_block + t_proj
         sample = (f"front end over {FRAMES} mel frames + sub linear + {blocks} of 24 blocks at T={T} + projector; "
                   f"24-block time = 24 x median block {t_block:.3f} s; total {total:.2f} s")
-    return {"value": AUDIO_S / total, "unit": "audio s/s", "cores": threads, "kind": "port", "sample": sample}
+    # calibration: the reference's CPU GEMM throughput shapes (src/cpu/gemm.rs
+    # throughput test: f32 weights, m x n x k) through the oracle's GEMM
+    gemm_rates = []
+    for m, n, k in ((2208, 4096, 1024), (2240, 4096, 1024), (448, 4096, 1024), (191, 4096, 1024),
+                    (191, 1024, 4096), (191, 3072, 1024)):
+        a = np.full((m, k), 0.01, np.float32)
+        w = oracle.PackW(np.full((n, k), 0.02, np.float32))
+        oracle.gemm(a[:8], w, threads=threads)
+        t0 = time.perf_counter()
+        oracle.gemm(a, w, threads=threads)
+        gemm_rates.append({"m": m, "n": n, "k": k, "gflops": 2.0 * m * n * k / (time.perf_counter() - t0) / 1e9})
+    return {"value": AUDIO_S / total, "unit": "audio s/s", "cores": threads, "kind": "port", "sample": sample,
+            "cpu_model": cpu_model(), "gemm_f32_throughput": gemm_rates}
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def traffic_workload(pkg, synth, torch) -> None:
@@ -346,7 +481,16 @@ def main() -> int:
         traffic_workload(pkg, synth, torch)
         return 0
 
-    dt, T, prof, dom, d, pipe = bench_encoder(pkg, synth, torch, args.steps, args.warmup)
+    enc, dt, T, prof, dom, d, pipe = bench_encoder(pkg, synth, torch, args.steps, args.warmup)
+    workloads = {}
+    workloads["configs4_batch16"] = bench_batch16(enc, pkg, synth, torch)
+    workloads["configs4_t15000"] = bench_long_stream(enc, pkg, synth, torch)
+    workloads["t188_lowbit"] = bench_t188(enc, pkg, synth, torch, lowbit=True)
+    enc.close()
+    workloads["configs2_t188_f16"] = bench_t188(None, pkg, synth, torch, lowbit=False)
+    for k, v in workloads.items():
+        log(f"[bench] {k}: " + ", ".join(f"{kk}={vv:.4g}" if isinstance(vv, float) else f"{kk}={vv}"
+                                          for kk, vv in v.items() if not isinstance(vv, dict)))
     # roofline of the dominant kernel from its launches inside the timed region
     # (every profiled label is one kernel, so this is rocprof's average duration)
     avg_s = d["ms"] / d["count"] / 1e3
@@ -357,6 +501,18 @@ def main() -> int:
     else:
         per_launch, peak, unit = d["bytes"] / d["count"], PEAK_HBM_GBS, "GB/s"
         achieved = per_launch / avg_s / 1e9
+    # the runner-up's roofline from the all-launch pass
+    second = sorted(prof, key=lambda k: -prof[k]["ms"])[1] if len(prof) > 1 else None
+    runner_up = None
+    if second is not None:
+        r = prof[second]
+        r_avg = r["ms"] / r["count"] / 1e3
+        r_mfma = r["flops"] > 0 and r["flops"] / r["bytes"] > PEAK_F16_TFLOPS / PEAK_HBM_GBS * 1e3
+        r_ach = (r["flops"] / r["count"] / r_avg / 1e12) if r_mfma else (r["bytes"] / r["count"] / r_avg / 1e9)
+        r_peak = PEAK_F16_TFLOPS if r_mfma else PEAK_HBM_GBS
+        runner_up = {"kernel": second, "bound": "mfma" if r_mfma else "hbm", "achieved": r_ach, "peak": r_peak,
+                     "unit": "TFLOP/s" if r_mfma else "GB/s", "frac": r_ach / r_peak, "avg_launch_us": r_avg * 1e6,
+                     "timing": "all-launch breakdown pass"}
     breakdown = {k: {"ms_per_step": v["ms"] / PROFILE_STEPS, "launches_per_step": v["count"] // PROFILE_STEPS,
                      "tflops": (v["flops"] / (v["ms"] / 1e3) / 1e12) if v["flops"] else None,
                      "gbs": v["bytes"] / (v["ms"] / 1e3) / 1e9}
@@ -418,7 +574,9 @@ def main() -> int:
         "roofline": {"kernel": dom, "bound": "mfma" if mfma_bound else "hbm", "achieved": achieved, "peak": peak,
                      "unit": unit, "frac": achieved / peak, "traffic": traffic,
                      ("flops_per_launch" if mfma_bound else "bytes_per_launch"): per_launch,
-                     "avg_launch_us": avg_s * 1e6},
+                     "avg_launch_us": avg_s * 1e6, "rule": "largest ms per step"},
+        "roofline_runner_up": runner_up,
+        "workloads": workloads,
         "breakdown": breakdown,
         "gemm_lowbit": gemm,
         "mel_frontend": mel,
