@@ -433,24 +433,32 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def traffic_workload(pkg, synth, torch) -> None:
-    """What the HBM-traffic counter passes profile (rocprofv3 --pmc FETCH_SIZE /
-    WRITE_SIZE -- python3 bench.py --traffic-workload): a 512 MiB device copy
-    whose bytes calibrate the counters, then two 1-block encodes at T=2207 (the
-    per-layer launches of the config-3 step)."""
+def traffic_workload(pkg, synth, torch, t: int = 2207, f16: bool = False) -> None:
+    """What the counter passes profile (rocprofv3 --pmc ... -- python3 bench.py
+    --traffic-workload [--traffic-t T] [--traffic-f16]): a 512 MiB device copy
+    whose bytes calibrate the traffic counters, then two encodes of a 1-block
+    encoder (4-bit, or f16 weights) on a synthetic log-mel giving T encoder
+    frames: front end, one block and projector, the per-layer launches of the
+    24-block step."""
     a = torch.empty(128 << 20, dtype=torch.float32, device="cuda")
     a.fill_(1.0)
     b = torch.empty_like(a)
     torch.cuda.synchronize()
     b.copy_(a)
     torch.cuda.synchronize()
-    src = synth.SynthCheckpoint(seed=0, n_layers=1, style="baseline", lowbit=True)
-    with pkg.HipEncoder.load_with(src, device=0, n_layers=1, front_end=False) as enc:
-        sub = np.random.default_rng(0).standard_normal((2207, 4096), dtype=np.float32)
-        enc.encode(sub, 2207)
-        enc.encode(sub, 2207)
+    del a, b
+    frames = 8 * t
+    while pkg.conv_len(pkg.conv_len(pkg.conv_len(frames))) > t:
+        frames -= 1
+    while pkg.conv_len(pkg.conv_len(pkg.conv_len(frames))) < t:
+        frames += 1
+    src = synth.SynthCheckpoint(seed=0, n_layers=1, style="baseline", lowbit=not f16)
+    with pkg.HipEncoder.load_with(src, device=0, n_layers=1) as enc:
+        mel = synth.mel(frames, seed=0)
+        enc.encode_mel(mel)
+        enc.encode_mel(mel)
     torch.cuda.synchronize()
-    log("[bench] traffic workload done")
+    log(f"[bench] traffic workload done (T={t}, {'f16' if f16 else '4-bit'} weights, {frames} mel frames)")
 
 
 def main() -> int:
@@ -462,7 +470,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-gemm", action="store_true")
     ap.add_argument("--traffic-workload", action="store_true",
-                    help="run only the workload of the HBM-traffic counter passes")
+                    help="run only the workload of the counter passes")
+    ap.add_argument("--traffic-t", type=int, default=2207, help="encoder frames of the counter workload")
+    ap.add_argument("--traffic-f16", action="store_true", help="counter workload with f16 weights")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -478,7 +488,7 @@ def main() -> int:
         return 1
 
     if args.traffic_workload:
-        traffic_workload(pkg, synth, torch)
+        traffic_workload(pkg, synth, torch, args.traffic_t, args.traffic_f16)
         return 0
 
     enc, dt, T, prof, dom, d, pipe = bench_encoder(pkg, synth, torch, args.steps, args.warmup)
