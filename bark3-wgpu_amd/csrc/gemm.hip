@@ -392,13 +392,13 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmParams p) {
   }
 }
 
-// Epilogue of a (32*FM) x 64 wave tile. Lane (l32, lhi) holds, for MFMA block (i, j), column
+// Epilogue of a (32*FM) x (32*NB) wave tile. Lane (l32, lhi) holds, for MFMA block (i, j), column
 // nw + 32j + l32 and rows m0 + 32i + 8g + 4lhi + b of acc[i][j][4g + b].
 // Column-dependent work (bias, head/dim split, output base) is done once
 // per column; row offsets are compile-time multiples of the row stride; a
 // tile inside M skips the per-row bound checks. bz selects the split-K slab.
-template <int FM, int EPI>
-__device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p, int m0, int nw, int bz, int lane,
+template <int FM, int EPI, int NB = 2>
+__device__ inline void tile_epilogue(floatx16 (&acc)[FM][NB], const GemmParams& p, int m0, int nw, int bz, int lane,
                                      int ib = 0, int ie = FM) {
   const int l32 = lane & 31, lhi = lane >> 5;
   EpiArgs ea = p.ea;
@@ -408,20 +408,21 @@ __device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p
   constexpr bool CHK = decltype(checked)::value;
   auto row_ok = [&](int rl) { return !CHK || mrow + rl < p.M; };  // rl = 32i + 8g + b
   if constexpr (EPI == (int)Epi::Glu) {
+    static_assert(NB == 2, "GLU pairs need both column blocks of a wave");
     float* base = ea.out_f32 + (size_t)mrow * ea.ldo + (nw >> 1) + l32;
 #pragma unroll
     for (int i = 0; i < FM; ++i) if (i >= ib && i < ie)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int rl = 32 * i + 8 * (v >> 2) + (v & 3);
-        if (row_ok(rl)) base[(size_t)rl * ea.ldo] = fast_sigmoid_mul(acc[i][0][v], acc[i][1][v]);
+        if (row_ok(rl)) base[(size_t)rl * ea.ldo] = fast_sigmoid_mul(acc[i][0][v], acc[i][NB - 1][v]);
       }
   } else if constexpr (EPI == (int)Epi::Qkv) {
     const int region = __builtin_amdgcn_readfirstlane(nw >> 10);  // 0 q, 1 k, 2 v (wave-uniform)
     if (region == 2) {
       // V^T[h][d][r]: a lane's four consecutive rows are contiguous, one 8-byte store
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NB; ++j) {
         const int hd = nw - 2048 + 32 * j + l32;  // h*128 + d
         half* vrow = ea.vt + (size_t)hd * ea.mp + mrow;
 #pragma unroll
@@ -442,7 +443,7 @@ __device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NB; ++j) {
         const int hd = (nw & 1023) + 32 * j + l32, h = hd >> 7, d = hd & 127;
         const size_t off = ((size_t)h * ea.mp + mrow) * HDIM + d;
         if (region == 0) {
@@ -473,7 +474,7 @@ __device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p
     }
   } else if constexpr (EPI == (int)Epi::RelK) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NB; ++j) {
       const int c = nw + 32 * j + l32, h = c >> 7, d = c & 127;
       half* pr = ea.rk + ((size_t)h * ea.pp + mrow) * HDIM + d;
 #pragma unroll
@@ -487,7 +488,7 @@ __device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p
   } else if constexpr (EPI == (int)Epi::StoreF16 || EPI == (int)Epi::StoreBF16 || EPI == (int)Epi::Silu ||
                        EPI == (int)Epi::BiasReluF16) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < NB; ++j) {
       const int c = nw + 32 * j + l32;
       const float bc = ea.bias ? ea.bias[c] : 0.0f;
       const size_t base = (size_t)mrow * ea.ldo + c;
@@ -517,7 +518,7 @@ __device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p
 #pragma unroll
     for (int i = 0; i < FM; ++i) if (i >= ib && i < ie)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int r = m0 + i * 32 + 8 * (v >> 2) + 4 * lhi + (v & 3);
@@ -532,9 +533,10 @@ __device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p
   else epilogue(std::integral_constant<bool, true>());
 }
 
-// Wide-tile kernel: workgroup tile (32*FM) x 64*WV, the WV waves (4, or 1
-// for short inputs, where 4-wave tiles would leave most CUs idle) side by
-// side, each owning all rows and 64 columns (FM x 2 MFMA blocks). Every output
+// Wide-tile kernel: workgroup tile (32*FM) x 32*NB*WV, the WV waves (4; 1
+// for short inputs, where 4-wave tiles would leave most CUs idle; 8 with one
+// column block each, NB = 1, for launches of one round of tiles) side by
+// side, each owning all rows and 32*NB columns (FM x NB MFMA blocks). Every output
 // element is one MFMA chain over its k in the same order whatever FM and WV
 // are, so the tile shape never changes results. B never
 // touches LDS: an MFMA B fragment is 8 consecutive k of one weight row, i.e.
@@ -549,16 +551,16 @@ __device__ inline void tile_epilogue(floatx16 (&acc)[FM][2], const GemmParams& p
 // K2ORD: accumulate slices 0-1 and 2-3 of every k-tile in two chains and add
 // them at the end, the two-group kernel's order (used for its epilogues, so
 // the tile shape still never changes results).
-template <int FM, bool LUT4, bool SWZ, bool ABF16, int EPI, int WV = 4, bool K2ORD = false>
-__global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_kernel(GemmParams p) {
-  constexpr int NT = 64 * WV;  // threads: WV waves of 64 columns each
+template <int FM, bool LUT4, bool SWZ, bool ABF16, int EPI, int WV = 4, bool K2ORD = false, int NB = 2>
+__global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4 && NB == 2) ? 2 : 1) gemm_wide_kernel(GemmParams p) {
+  constexpr int NT = 64 * WV;  // threads: WV waves of 32 * NB columns each
   constexpr int BM = 32 * FM;
   constexpr int A_CH = BM * BK / 8 / NT;  // 16-byte chunks of A per thread per k-tile
-  constexpr int B_V = LUT4 ? 2 : 8;        // 16-byte loads of B per lane per k-tile
+  constexpr int B_V = LUT4 ? NB : 4 * NB;  // 16-byte loads of B per lane per k-tile
   // 4-bit tiles of up to 128 rows keep two workgroups per CU (two waves per
   // SIMD, so one wave's code expansion overlaps the other's MFMAs): that needs
   // <= 256 registers per lane, hence two register stages of A and B.
-  constexpr bool OCC2 = LUT4 && FM <= 4;
+  constexpr bool OCC2 = LUT4 && FM <= 4 && NB == 2;
   constexpr int BD = (LUT4 && !OCC2) ? 4 : 2;  // k-tiles of B in flight (register stages)
   constexpr int AD = (FM >= 6 || OCC2) ? 2 : 4;  // k-tiles of A in flight (register stages)
   __shared__ __attribute__((aligned(16))) half As[2][BM * LDK];
@@ -576,8 +578,8 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_
   const int xq = G / 8, xr = G % 8, xcd = bid % 8;
   const int tix = xcd * xq + min(xcd, xr) + bid / 8;
   const int bz = tix / (gx * gy), by = (tix / gx) % gy, bx = tix % gx;
-  const int n0 = bx * NT, m0 = by * BM;
-  const int nw = n0 + wid * 64;
+  const int n0 = bx * (32 * NB * WV), m0 = by * BM;
+  const int nw = n0 + wid * 32 * NB;
   // K chunk of this split: whole 256-k units, the first K/256 % splits
   // chunks one unit longer (depends on K and the split count only)
   const int kunits = p.K / 256, kq = kunits / p.splits, kr = kunits % p.splits;
@@ -586,12 +588,12 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_
 
   // Global addresses are a wave-uniform base plus 32-bit lane offsets (the
   // host checks the operands fit), so loads use scalar base registers.
-  RowLut lut[2];
+  RowLut lut[NB];
   const uint8_t* bbase = LUT4 ? p.codes + kz0 / 2 : reinterpret_cast<const uint8_t*>(p.W + kz0);
   constexpr int B_ROW_BYTES_PER_K2 = LUT4 ? 1 : 4;  // bytes per row per 2 k
-  uint32_t boff[2];  // this lane's B bytes of k-tile 0, for its two rows
+  uint32_t boff[NB];  // this lane's B bytes of k-tile 0, for its rows
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < NB; ++j) {
     const int n = nw + 32 * j + l32;
     if constexpr (LUT4) lut[j] = load_row_lut(p.lut + (size_t)n * 16);
     boff[j] = (uint32_t)n * (uint32_t)(p.K / 2 * B_ROW_BYTES_PER_K2) + (LUT4 ? 16 : 64) * lhi;
@@ -630,9 +632,9 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_
     kt = min(kt, nk - 1);
     const uint8_t* bt = bbase + (size_t)kt * B_TILE_BYTES;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int q = 0; q < B_V / 2; ++q) b.v[j * (B_V / 2) + q] = *reinterpret_cast<const uint4*>(bt + boff[j] + 16 * q);
+      for (int q = 0; q < B_V / NB; ++q) b.v[j * (B_V / NB) + q] = *reinterpret_cast<const uint4*>(bt + boff[j] + 16 * q);
   };
   auto store_chunk = [&](int buf, const AStage& a, int i) {
     if constexpr (ABF16) {
@@ -650,18 +652,18 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_
     }
   };
 
-  floatx16 acc[FM][2], acc_hi[K2ORD ? FM : 1][2];
+  floatx16 acc[FM][NB], acc_hi[K2ORD ? FM : 1][NB];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
   if constexpr (K2ORD)
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc_hi[i][j][v] = 0.0f;
 
@@ -690,12 +692,12 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_
   // load queue with the matrix core idle.
   auto tile = [&](int cur, int nxt, const BStage& bs, const AStage& as, int ka, AStage& ad, int kb, BStage& bd) {
     half8 af[2][FM];
-    half8 bf[2][2];
-    constexpr int VEXP = LUT4 ? 50 : 1;  // VALU instructions of two code expansions
-    constexpr int VPER = (VEXP + 2 * FM - 1) / (2 * FM);
+    half8 bf[2][NB];
+    constexpr int VEXP = LUT4 ? 25 * NB : 1;  // VALU instructions of the slice's code expansions
+    constexpr int VPER = (VEXP + NB * FM - 1) / (NB * FM);
     read_af(af[0], cur, 0);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) bf[0][j] = b_frag(bs, j, 0);
+    for (int j = 0; j < NB; ++j) bf[0][j] = b_frag(bs, j, 0);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int c = s & 1, n = c ^ 1;
@@ -706,7 +708,7 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_
       __builtin_amdgcn_sched_barrier(0);
       if (s < 3) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) bf[n][j] = b_frag(bs, j, s + 1);
+        for (int j = 0; j < NB; ++j) bf[n][j] = b_frag(bs, j, s + 1);
       }
 #pragma unroll
       for (int i = 0; i < A_CH; ++i)
@@ -725,7 +727,7 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < NB; ++j) {
           if (K2ORD && s >= 2)
             acc_hi[K2ORD ? i : 0][j] =
                 __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc_hi[K2ORD ? i : 0][j], 0, 0, 0);
@@ -733,7 +735,7 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
         }
 #pragma unroll
-      for (int m = 0; m < 2 * FM; ++m) {
+      for (int m = 0; m < NB * FM; ++m) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         if (s < 3) __builtin_amdgcn_sched_group_barrier(0x002, VPER, 0);
         if (m < nvm) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
@@ -772,11 +774,11 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4) ? 2 : 1) gemm_wide_
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NB; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] += acc_hi[i][j][v];
 
-  tile_epilogue<FM, EPI>(acc, p, m0, nw, bz, lane);
+  tile_epilogue<FM, EPI, NB>(acc, p, m0, nw, bz, lane);
 }
 
 // Two-group tile kernel: 512 threads = two K-groups of four waves. Wave
@@ -1487,9 +1489,10 @@ bool wide_supported(Epi epi, int fmt) {
   }
 }
 
-template <int FM, int WV = 4, bool K2ORD = false>
+template <int FM, int WV = 4, bool K2ORD = false, int NB = 2>
 void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t s) {
-  dim3 grid(p.N / (64 * WV), ceil_div(p.M, 32 * FM), p.splits), block(64 * WV);
+  BARK_REQUIRE(p.N % (32 * NB * WV) == 0, "gemm: N is not a multiple of the wide tile");
+  dim3 grid(p.N / (32 * NB * WV), ceil_div(p.M, 32 * FM), p.splits), block(64 * WV);
   if constexpr (K2ORD) {  // the two-group kernel's default epilogue only
     BARK_REQUIRE(epi == Epi::Silu && fmt != 2, "gemm: no two-group-order wide kernel for this epilogue");
     if (fmt == 0) BARK_LAUNCH((gemm_wide_kernel<FM, false, false, false, (int)Epi::Silu, WV, true>), grid, block, 0, s, p);
@@ -1497,7 +1500,7 @@ void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t 
     return;
   }
 #define BARK_K(L4, SW, AB, E) \
-  BARK_LAUNCH((gemm_wide_kernel<FM, L4, SW, AB, (int)Epi::E, WV>), grid, block, 0, s, p)
+  BARK_LAUNCH((gemm_wide_kernel<FM, L4, SW, AB, (int)Epi::E, WV, false, NB>), grid, block, 0, s, p)
 #define BARK_CASE(E)                                   \
   case Epi::E:                                         \
     if (fmt == 0) BARK_K(false, false, false, E);      \
@@ -1513,6 +1516,13 @@ void launch_wide(const GemmParams& p, Epi epi, int fmt, bool abf16, hipStream_t 
       BARK_PLAIN(StoreF32)
       BARK_PLAIN(StoreF16)
       BARK_PLAIN(StoreBF16)
+      default:
+        break;
+    }
+  } else if constexpr (NB == 1) {  // one column block per wave: the epilogues tall_supported names
+    switch (epi) {
+      BARK_CASE(StoreF32)
+      BARK_CASE(Qkv)
       default:
         break;
     }
@@ -1755,6 +1765,33 @@ int pick_narrow_fm(int M, int N, int splits) {
   return (long)ceil_div(M, 32) * (N / 64) * splits <= 1024 ? 1 : 2;
 }
 
+// Eight-wave tiles (128 x 256, each wave 128 rows x one 32-column block):
+// where the 128-row tiles of a launch fit the 256 CUs in one round (and fill
+// at least half of them), a workgroup per CU with two waves per SIMD beats the
+// four-wave tiles, whose workgroups then sit one wave per SIMD. Measured on
+// MI355X at T = 2207 (per launch): qkv 27.2 -> 22.9 us, FFN down 29.7 ->
+// 28.3, the K = 1024 residual linears 15.7 -> 13.9-14.1. Per-element order
+// is the wide kernel's (one chain per element), so results do not change.
+// BARK_HIP_GEMM_TALL = 0 turns it off.
+bool tall_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("BARK_HIP_GEMM_TALL");
+    return !(e && atoi(e) == 0);
+  }();
+  return on;
+}
+
+bool tall_fits(int M, int N, int splits) {
+  if (!tall_enabled() || N % 256 != 0) return false;
+  const long tiles = (long)ceil_div(M, 128) * (N / 256) * splits;
+  return tiles >= 128 && tiles <= 256;
+}
+
+bool tall_supported(Epi epi, int fmt) {
+  if (fmt == 2) return epi == Epi::StoreF32 || epi == Epi::StoreF16 || epi == Epi::StoreBF16;
+  return epi == Epi::StoreF32 || epi == Epi::Qkv;
+}
+
 void launch_fm(int fm, int narrow, const GemmParams& p, Epi epi, int fmt, bool a_bf16, hipStream_t stream,
                bool k2ord = false) {
   if (narrow >= 1 && k2ord) launch_wide<1, 1, true>(p, epi, fmt, a_bf16, stream);
@@ -1800,6 +1837,11 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   const int narrow = W.n % 256 == 0 && fits32 && wide_supported(epi, fmt) && (!k2 || epi == Epi::Silu)
                          ? pick_narrow_fm(M, W.n, 1)
                          : 0;
+  if (!narrow && !k2 && fits32 && tall_supported(epi, fmt) && tall_fits(M, W.n, 1)) {
+    launch_wide<4, 8, false, 1>(p, epi, fmt, a_bf16, stream);
+    BARK_HIP_CHECK(hipGetLastError());
+    return;
+  }
   if (narrow) {  // the two-chain order at 64 rows spills: one row block there
     launch_fm(0, k2 ? 1 : narrow, p, epi, fmt, a_bf16, stream, k2);
     BARK_HIP_CHECK(hipGetLastError());
@@ -1848,6 +1890,11 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
   GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, splits, (size_t)M * ldo};
   const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
   const int narrow = k2_default(Epi::StoreF32) ? 0 : pick_narrow_fm(M, W.n, splits);
+  if (!narrow && !k2_default(Epi::StoreF32) && tall_supported(Epi::StoreF32, fmt) && tall_fits(M, W.n, splits)) {
+    launch_wide<4, 8, false, 1>(p, Epi::StoreF32, fmt, a_bf16, stream);
+    BARK_HIP_CHECK(hipGetLastError());
+    return;
+  }
   if (k2_default(Epi::StoreF32)) {
     const int fm2 = pick_k2_fm(M, W.n, splits);
     if (fm2) {
