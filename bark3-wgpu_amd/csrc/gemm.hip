@@ -781,6 +781,156 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4 && NB == 2) ? 2 : 1)
   tile_epilogue<FM, EPI, NB>(acc, p, m0, nw, bz, lane);
 }
 
+// Column-strip kernel for short inputs: a workgroup holds MW waves, one per
+// 32-row block of a (32*MW)-row tile (blockIdx.y), and covers 32*NB columns
+// (blockIdx.x) of one K chunk (blockIdx.z, chunked as in gemm_wide_kernel).
+// Each k-tile's weight fragments (4 slices x NB column blocks, 1 KB each) are
+// made ONCE per workgroup — fragment f by wave f % MW: expanded from the
+// 4-bit codes with the row tables, or copied for f16 weights — into LDS, where
+// every wave reads them; the A tile is staged through LDS from coalesced row
+// loads (A fragments loaded straight from global memory touch 32 partial
+// cache lines per instruction and measured 40 % slower). The one-wave wide tiles expand
+// every code word once per 32 rows instead. Per-element order is the wide
+// kernel's (k-tiles ascending, slices 0..3, lane half h of slice s covering
+// k = 32h + 8s .. +7; K2ORD: slices 0-1 and 2-3 in two chains added at the
+// end), so results are bit-identical to it. One barrier per k-tile: tile
+// kt + 1's fragments go to the other LDS buffer while tile kt's are read.
+template <bool LUT4, int EPI, int NB, bool K2ORD>
+__global__ void __launch_bounds__(512) gemm_strip_kernel(GemmParams p) {
+  constexpr int NF = 4 * NB;   // weight fragments per k-tile
+  constexpr int FPW = 2 * NB;  // fragments one wave makes at most (MW >= 2)
+  constexpr int SD = 4;        // k-tiles of A and weights in flight (register stages)
+  __shared__ __attribute__((aligned(16))) uint4 Bs[2][NF][64];
+  __shared__ __attribute__((aligned(16))) half As[2][256 * LDK];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int MW = blockDim.x >> 6;
+  const int l32 = lane & 31, lhi = lane >> 5;
+  const int n0 = blockIdx.x * 32 * NB, bz = blockIdx.z;
+  const int m0 = (blockIdx.y * MW + wid) * 32;
+  const int kunits = p.K / 256, kq = kunits / p.splits, kr = kunits % p.splits;
+  const int kz0 = 256 * (bz * kq + min(bz, kr));
+  const int nk = 4 * (kq + (bz < kr ? 1 : 0));  // k-tiles of this chunk
+
+  // A staging: thread t loads 16-byte chunk t % 8 of rows t / 8 + 8 MW i
+  // (i < 4) of the workgroup's rows (rows past M repeat row M - 1)
+  const int wrow0 = blockIdx.y * MW * 32, arow = threadIdx.x >> 3, acol = (threadIdx.x & 7) * 8;
+  const half* abase[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    abase[i] = p.A + (size_t)min(wrow0 + arow + 8 * MW * i, p.M - 1) * p.lda + kz0 + acol;
+  const int af_off = (32 * wid + l32) * LDK + 32 * lhi;  // this lane's A fragments
+  // weight data of the fragments this wave makes: fragment f = wid + MW * i
+  // is column block j = f / 4, slice s = f % 4 of every k-tile
+  // (the slice is a runtime value, so its code word is addressed in the load:
+  // picking a word of a loaded vector by a runtime index goes through scratch)
+  RowLut lut[FPW];
+  const uint8_t* wsrc[FPW];
+#pragma unroll
+  for (int i = 0; i < FPW; ++i) {
+    const int f = min(wid + MW * i, NF - 1), j = f >> 2, n = n0 + 32 * j + l32;
+    if constexpr (LUT4) {
+      lut[i] = load_row_lut(p.lut + (size_t)n * 16);
+      wsrc[i] = p.codes + (size_t)n * (p.K / 2) + kz0 / 2 + 16 * lhi + 4 * (f & 3);  // 32 bytes per k-tile
+    } else {
+      wsrc[i] = reinterpret_cast<const uint8_t*>(p.W + (size_t)n * p.K + kz0 + 32 * lhi) + 16 * (f & 3);
+    }
+  }
+  const int nmine = (NF - wid + MW - 1) / MW;  // fragments this wave makes
+
+  // register stages: named variables, rotated by an unconditional four-tile
+  // loop body (K chunks are whole 256-k units); their values reach LDS through
+  // element-wise copies (a whole-member store through a cast pointer kept
+  // every stage in scratch memory)
+  using BW = std::conditional_t<LUT4, uint32_t, uint4>;  // one code word, or 8 f16 weights
+  struct Stage {
+    uint4 a[4];
+    BW b[FPW];
+  };
+  Stage r0, r1, r2, r3;
+  auto load = [&](int kt, Stage& st) __attribute__((always_inline)) {
+    kt = min(kt, nk - 1);  // loads past the last k-tile re-read it
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st.a[i] = *reinterpret_cast<const uint4*>(abase[i] + kt * BK);
+#pragma unroll
+    for (int i = 0; i < FPW; ++i)
+      if (i < nmine) st.b[i] = *reinterpret_cast<const BW*>(wsrc[i] + kt * (LUT4 ? BK / 2 : BK * 2));
+  };
+  auto make = [&](int buf, const Stage& st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) {
+      if (i < nmine) {
+        if constexpr (LUT4) {
+          Bs[buf][wid + MW * i][lane] = expand8<true>(st.b[i], lut[i]);
+        } else {
+          const uint4 t{st.b[i].x, st.b[i].y, st.b[i].z, st.b[i].w};
+          Bs[buf][wid + MW * i][lane] = t;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 t{st.a[i].x, st.a[i].y, st.a[i].z, st.a[i].w};
+      *reinterpret_cast<uint4*>(&As[buf][(arow + 8 * MW * i) * LDK + acol]) = t;
+    }
+  };
+
+  floatx16 acc[1][NB], acc_hi[K2ORD ? NB : 1];
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[0][j][v] = 0.0f;
+  if constexpr (K2ORD)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc_hi[j][v] = 0.0f;
+
+  auto mfmas = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const half8 af = ld_half8(&As[buf][af_off + 8 * s]);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const uint4 b4 = Bs[buf][4 * j + s][lane];
+        const half8 bf = *reinterpret_cast<const half8*>(&b4);
+        if (K2ORD && s >= 2)
+          acc_hi[K2ORD ? j : 0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc_hi[K2ORD ? j : 0], 0, 0, 0);
+        else
+          acc[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf, acc[0][j], 0, 0, 0);
+      }
+    }
+  };
+
+  // k-tile kt lives in register stage kt % 4 and LDS buffer kt % 2; past the
+  // last tile, loads re-read it and the fragments made go to a buffer that is
+  // never read again
+  auto iter = [&](int kt, Stage& cur, const Stage& next) __attribute__((always_inline)) {
+    load(kt + SD, cur);  // stage kt % 4's tile kt is already in LDS
+    make((kt + 1) & 1, next);
+    mfmas(kt & 1);
+    __syncthreads();
+  };
+  load(0, r0);
+  load(1, r1);
+  load(2, r2);
+  load(3, r3);
+  make(0, r0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += SD) {
+    iter(kt, r0, r1);
+    iter(kt + 1, r1, r2);
+    iter(kt + 2, r2, r3);
+    iter(kt + 3, r3, r0);
+  }
+  if constexpr (K2ORD)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[0][j][v] += acc_hi[j][v];
+  if (m0 >= p.M) return;  // a wave past the last row (no barrier follows)
+  tile_epilogue<1, EPI, NB>(acc, p, m0, n0, bz, lane);
+}
+
 // Two-group tile kernel: 512 threads = two K-groups of four waves. Wave
 // (g, w) computes the same (32*FM) x 64 tile as wave w of gemm_wide_kernel;
 // of every 64-k tile, group g runs the 16-k slices 2g and 2g + 1 (k = 32h +
@@ -1765,6 +1915,60 @@ int pick_narrow_fm(int M, int N, int splits) {
   return (long)ceil_div(M, 32) * (N / 64) * splits <= 1024 ? 1 : 2;
 }
 
+// Column-strip kernel launches: one 32-column block per workgroup, MW waves
+// of 32 rows each (2..8). f16 weights (fmt 0) and swizzled 4-bit weights (fmt 1).
+template <int NB, bool K2ORD>
+void launch_strip(const GemmParams& p, Epi epi, int fmt, int mw, hipStream_t s) {
+  static_assert(NB == 1, "one column block per strip");
+  BARK_REQUIRE(mw >= 2 && mw <= 8 && p.N % (32 * NB) == 0 && fmt != 2, "gemm: bad strip launch");
+  dim3 grid(p.N / (32 * NB), ceil_div(p.M, 32 * mw), p.splits), block(64 * mw);
+#define BARK_SK(E)                                                                                         \
+  do {                                                                                                     \
+    if (fmt == 0) BARK_LAUNCH((gemm_strip_kernel<false, (int)Epi::E, NB, K2ORD>), grid, block, 0, s, p); \
+    else BARK_LAUNCH((gemm_strip_kernel<true, (int)Epi::E, NB, K2ORD>), grid, block, 0, s, p);          \
+  } while (0)
+  if constexpr (K2ORD) {
+    BARK_REQUIRE(epi == Epi::Silu, "gemm: no two-chain strip kernel for this epilogue");
+    BARK_SK(Silu);
+  } else {
+    switch (epi) {
+      case Epi::StoreF32: BARK_SK(StoreF32); break;
+      case Epi::Silu: BARK_SK(Silu); break;
+      case Epi::Qkv: BARK_SK(Qkv); break;
+      default: throw Error{"gemm: no strip kernel for this epilogue"};
+    }
+  }
+#undef BARK_SK
+}
+
+// Waves per strip workgroup (0: the strip kernel does not apply), for
+// 33 <= M <= 256: one wave per 32-row block of a row tile, with the rows cut
+// into as many equal tiles (of two blocks or more) as keep the launch within
+// one workgroup per CU: more tiles fill more CUs, each tile making its own
+// weight fragments. BARK_HIP_GEMM_STRIP = 0 turns the kernel off.
+int strip_waves(int M, int N, int splits, Epi epi, int fmt) {
+  static const int forced = [] {
+    const char* e = getenv("BARK_HIP_GEMM_STRIP");
+    return e ? atoi(e) : -1;
+  }();
+  if (forced == 0 || fmt == 2 || M <= 32 || M > 256) return 0;
+  // GLU needs both halves of a pair in one wave (two column blocks): its
+  // strips are too few to fill the CUs (measured slower than the one-wave
+  // tiles at T = 188), so it stays there
+  if (epi != Epi::StoreF32 && epi != Epi::Silu && epi != Epi::Qkv) return 0;
+  const long strips = (long)(N / 32) * splits;
+  const int rb = ceil_div(M, 32);  // 32-row blocks
+  int mw = rb < 2 ? 2 : rb;
+  for (int rt = 2; rt <= rb / 2; ++rt)  // row tiles of at least two blocks
+    if ((long)rt * strips <= 256) mw = ceil_div(rb, rt);
+  return mw;
+}
+
+void launch_strip_for(const GemmParams& p, Epi epi, int fmt, int mw, bool k2ord, hipStream_t s) {
+  if (k2ord) launch_strip<1, true>(p, epi, fmt, mw, s);
+  else launch_strip<1, false>(p, epi, fmt, mw, s);
+}
+
 // Eight-wave tiles (128 x 256, each wave 128 rows x one 32-column block):
 // where the 128-row tiles of a launch fit the 256 CUs in one round (and fill
 // at least half of them), a workgroup per CU with two waves per SIMD beats the
@@ -1837,6 +2041,12 @@ void gemm(const half* A, int lda, int M, const GemmWeight& W, Epi epi, const Epi
   const int narrow = W.n % 256 == 0 && fits32 && wide_supported(epi, fmt) && (!k2 || epi == Epi::Silu)
                          ? pick_narrow_fm(M, W.n, 1)
                          : 0;
+  const int mw = W.n % 256 == 0 && fits32 ? strip_waves(M, W.n, 1, epi, fmt) : 0;
+  if (mw) {  // short inputs: weight fragments made once per workgroup
+    launch_strip_for(p, epi, fmt, mw, k2 && epi == Epi::Silu, stream);
+    BARK_HIP_CHECK(hipGetLastError());
+    return;
+  }
   if (!narrow && !k2 && fits32 && tall_supported(epi, fmt) && tall_fits(M, W.n, 1)) {
     launch_wide<4, 8, false, 1>(p, epi, fmt, a_bf16, stream);
     BARK_HIP_CHECK(hipGetLastError());
@@ -1890,6 +2100,12 @@ void gemm_split(const half* A, int lda, int M, const GemmWeight& W, int splits, 
   GemmParams p{A, lda, W.w16, W.codes, W.lut, M, W.n, W.k, ea, splits, (size_t)M * ldo};
   const int fmt = !W.lut4() ? 0 : W.swizzled ? 1 : 2;
   const int narrow = k2_default(Epi::StoreF32) ? 0 : pick_narrow_fm(M, W.n, splits);
+  const int mw = strip_waves(M, W.n, splits, Epi::StoreF32, fmt);
+  if (mw) {
+    launch_strip_for(p, Epi::StoreF32, fmt, mw, false, stream);
+    BARK_HIP_CHECK(hipGetLastError());
+    return;
+  }
   if (!narrow && !k2_default(Epi::StoreF32) && tall_supported(Epi::StoreF32, fmt) && tall_fits(M, W.n, splits)) {
     launch_wide<4, 8, false, 1>(p, Epi::StoreF32, fmt, a_bf16, stream);
     BARK_HIP_CHECK(hipGetLastError());

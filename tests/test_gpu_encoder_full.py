@@ -190,6 +190,24 @@ def test_batch_equals_individual(pkg, synth):
         assert np.array_equal(b, s)
 
 
+def test_short_inputs_equal_their_batched_rows(pkg, synth):
+    """Inputs of at most 256 frames run the short-input GEMM tiles (weight
+    fragments made once per workgroup, 4-bit and f16 weights alike); packed
+    with a long one they run the long-input tiles. The per-element MFMA order
+    is the same, so the results are identical bit for bit."""
+    frames = [1500, 800, 300, 4000]  # T = 188, 100, 38, 500
+    for lowbit in (True, False):
+        print(f"case short vs batched frames={frames} lowbit={lowbit}", flush=True)
+        src = synth.SynthCheckpoint(seed=43, n_layers=2, style="rich", lowbit=lowbit)
+        mels = [synth.mel(f, seed=10 + i) for i, f in enumerate(frames)]
+        with pkg.HipEncoder.load_with(src, n_layers=2) as enc:
+            batch = enc.encode_mel_batch(mels)
+            singles = [enc.encode_mel(m)[0] for m in mels]
+        for b, s in zip(batch, singles):
+            assert b.shape == s.shape
+            assert np.array_equal(b, s)
+
+
 def test_n_valid_masks_front_end(pkg, synth, oracle):
     """n_valid < n_frames zeroes the masked frames after each strided conv
     (src/sub.rs:259-273)."""
