@@ -104,6 +104,23 @@ __device__ inline uint4 expand8(uint32_t w, const RowLut& t) {
   }
 }
 
+// bf16 -> f16 of 8 consecutive k (exact for |x| in the f16 normal range),
+// stored in the k order 0, 2, 4, 6, 1, 3, 5, 7: the order expand8<true> gives
+// a plain-layout code word (byte j = codes 2j, 2j + 1 read as codes j, j + 4).
+// An MFMA sums the same products whatever the order of its operands' k, so
+// bf16 activations staged this way meet plain 4-bit weights expanded with the
+// swizzled layout's cheaper permutes; the conversion's placement is free.
+__device__ inline half8 bf16x8_to_f16_eo(uint4 x) {
+  const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
+  half8 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = (half)__uint_as_float(w4[e] << 16);
+    v[4 + e] = (half)__uint_as_float(w4[e] & 0xffff0000u);
+  }
+  return v;
+}
+
 // f32 -> f16 after materialising the f32 value: the compiler may otherwise
 // fuse a multiply with the conversion (one rounding) in some epilogue
 // instantiations and not in others, which would make a row's f16 output
@@ -554,6 +571,9 @@ __device__ inline void tile_epilogue(floatx16 (&acc)[FM][NB], const GemmParams& 
 template <int FM, bool LUT4, bool SWZ, bool ABF16, int EPI, int WV = 4, bool K2ORD = false, int NB = 2>
 __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4 && NB == 2) ? 2 : 1) gemm_wide_kernel(GemmParams p) {
   constexpr int NT = 64 * WV;  // threads: WV waves of 32 * NB columns each
+  // plain 4-bit codes with bf16 activations (the isolated linear): A chunks
+  // converted in the order the swizzled expansion gives plain codes
+  constexpr bool EO = LUT4 && !SWZ && ABF16;
   constexpr int BM = 32 * FM;
   constexpr int A_CH = BM * BK / 8 / NT;  // 16-byte chunks of A per thread per k-tile
   constexpr int B_V = LUT4 ? NB : 4 * NB;  // 16-byte loads of B per lane per k-tile
@@ -637,7 +657,9 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4 && NB == 2) ? 2 : 1)
       for (int q = 0; q < B_V / NB; ++q) b.v[j * (B_V / NB) + q] = *reinterpret_cast<const uint4*>(bt + boff[j] + 16 * q);
   };
   auto store_chunk = [&](int buf, const AStage& a, int i) {
-    if constexpr (ABF16) {
+    if constexpr (EO) {
+      st_half8(&As[buf][a_lds[i]], bf16x8_to_f16_eo(uint4{a.v[i].x, a.v[i].y, a.v[i].z, a.v[i].w}));
+    } else if constexpr (ABF16) {
       const uint32_t w4[4] = {a.v[i].x, a.v[i].y, a.v[i].z, a.v[i].w};
       half8 v;
 #pragma unroll
@@ -677,7 +699,7 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4 && NB == 2) ? 2 : 1)
   auto b_frag = [&](const BStage& b, int j, int s) {
     uint4 q;
     if constexpr (LUT4) {
-      q = expand8<SWZ>(code_word(b.v[j], s), lut[j]);
+      q = expand8<SWZ || EO>(code_word(b.v[j], s), lut[j]);
     } else {
       q = uint4{b.v[4 * j + s].x, b.v[4 * j + s].y, b.v[4 * j + s].z, b.v[4 * j + s].w};
     }
@@ -1454,7 +1476,8 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const float* part, in
 // chunk (32 * MB rows x 64 k) through its own LDS region: loaded row by row
 // (eight rows of 128 bytes per load instruction, where fragment-shaped loads
 // touch 32-64 cache lines each and ran at the vector L1's line rate),
-// converted from bf16 on the way when needed, and read back as MFMA
+// converted from bf16 on the way when needed (in the k order that lets the
+// plain codes take the swizzled expansion, bf16x8_to_f16_eo), and read back as MFMA
 // fragments. The next chunk's codes and activations are in flight meanwhile.
 // Rows are split over workgroups, never K, so no partial sums leave the
 // workgroup (a K split finished by the last-arriving workgroup needed an
@@ -1467,17 +1490,6 @@ struct SkinnyArgs {
   void* out;
   int out_kind;  // 0 f32, 1 f16, 2 bf16
 };
-
-__device__ inline half8 bf16x8_to_f16(uint4 x) {  // exact for |x| in the f16 normal range
-  const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
-  half8 v;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    v[2 * e] = (half)__uint_as_float(w4[e] << 16);
-    v[2 * e + 1] = (half)__uint_as_float(w4[e] & 0xffff0000u);
-  }
-  return v;
-}
 
 // rows m, columns n .. n + 3 of C from one lane's four accumulators
 __device__ inline void skinny_store4(const SkinnyArgs& s, int m, int n, floatx4 v) {
@@ -1548,7 +1560,7 @@ __global__ void __launch_bounds__(256, 2) gemm_skinny_kernel(SkinnyArgs s) {
     wave_sync();  // the previous chunk's fragment reads are done
 #pragma unroll
     for (int i = 0; i < LD_PER; ++i) {
-      const half8 v = ABF16 ? bf16x8_to_f16(ar[i]) : __builtin_bit_cast(half8, ar[i]);
+      const half8 v = ABF16 ? bf16x8_to_f16_eo(ar[i]) : __builtin_bit_cast(half8, ar[i]);
       st_half8(st + (8 * i + sr) * SK_LD + sc, v);
     }
     const uint32_t words[4] = {cw.x, cw.y, cw.z, cw.w};
@@ -1558,7 +1570,7 @@ __global__ void __launch_bounds__(256, 2) gemm_skinny_kernel(SkinnyArgs s) {
     }
     half8 wf[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) wf[c] = __builtin_bit_cast(half8, expand8<false>(words[c], lut));
+    for (int c = 0; c < 4; ++c) wf[c] = __builtin_bit_cast(half8, expand8<ABF16>(words[c], lut));
     wave_sync();  // the staged rows are visible to the whole wave
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
