@@ -1927,11 +1927,11 @@ int pick_narrow_fm(int M, int N, int splits) {
   return (long)ceil_div(M, 32) * (N / 64) * splits <= 1024 ? 1 : 2;
 }
 
-// Column-strip kernel launches: one 32-column block per workgroup, MW waves
-// of 32 rows each (2..8). f16 weights (fmt 0) and swizzled 4-bit weights (fmt 1).
+// Column-strip kernel launches: NB 32-column blocks per workgroup (one, see
+// strip_waves), MW waves of 32 rows each (2..8). f16 weights (fmt 0) and
+// swizzled 4-bit weights (fmt 1).
 template <int NB, bool K2ORD>
 void launch_strip(const GemmParams& p, Epi epi, int fmt, int mw, hipStream_t s) {
-  static_assert(NB == 1, "one column block per strip");
   BARK_REQUIRE(mw >= 2 && mw <= 8 && p.N % (32 * NB) == 0 && fmt != 2, "gemm: bad strip launch");
   dim3 grid(p.N / (32 * NB), ceil_div(p.M, 32 * mw), p.splits), block(64 * mw);
 #define BARK_SK(E)                                                                                         \
@@ -1968,6 +1968,9 @@ int strip_waves(int M, int N, int splits, Epi epi, int fmt) {
   // strips are too few to fill the CUs (measured slower than the one-wave
   // tiles at T = 188), so it stays there
   if (epi != Epi::StoreF32 && epi != Epi::Silu && epi != Epi::Qkv) return 0;
+  // (measured on MI355X at T = 188: strips of two column blocks, which halve
+  // the activation re-reads, ran 1.3-1.5x slower; allowing two workgroups per
+  // CU, 512 per launch, 3 % slower)
   const long strips = (long)(N / 32) * splits;
   const int rb = ceil_div(M, 32);  // 32-row blocks
   int mw = rb < 2 ? 2 : rb;
