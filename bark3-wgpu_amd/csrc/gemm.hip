@@ -926,10 +926,17 @@ __global__ void __launch_bounds__(512) gemm_strip_kernel(GemmParams p) {
   // k-tile kt lives in register stage kt % 4 and LDS buffer kt % 2; past the
   // last tile, loads re-read it and the fragments made go to a buffer that is
   // never read again
+  // the tile's MFMAs are issued first and the next tile's fragments (the
+  // other LDS buffer) are made between them
   auto iter = [&](int kt, Stage& cur, const Stage& next) __attribute__((always_inline)) {
     load(kt + SD, cur);  // stage kt % 4's tile kt is already in LDS
-    make((kt + 1) & 1, next);
     mfmas(kt & 1);
+    make((kt + 1) & 1, next);
+#pragma unroll
+    for (int m = 0; m < 4 * NB; ++m) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, LUT4 ? 8 : 1, 0);  // a few VALU
+    }
     __syncthreads();
   };
   load(0, r0);
