@@ -323,6 +323,9 @@ struct BarkHip {
   // position table rows for pos = pos_t-1 .. -(pos_t-1), f16, plus zero rows
   DevBuf pos;
   int pos_t = 0;
+  // rk holds every layer's relative keys for all rows of the position table
+  // as of pos_t == relk_t (0: not computed); see encoder_blocks
+  int relk_t = 0;
 
   // workspace
   DevBuf sub16, xn, hid, qu, qv, kh, vt, rk, ao, h, h2, glu, pooler, dump, bounds, tiles;
@@ -754,7 +757,6 @@ struct BarkHip {
 
   void ensure_workspace(const Plan& pl) {
     const size_t mp = pl.mp;
-    const size_t pp = round_up(2 * pl.tc - 1, 64);
     ensure(sub16, mp * 4096 * 2);
     ensure(xn, mp * HIDDEN * 2);
     ensure(hid, mp * FFN * 2);
@@ -762,7 +764,12 @@ struct BarkHip {
     ensure(qv, HEADS * mp * HDIM * 2);
     ensure(kh, HEADS * mp * HDIM * 2);
     ensure(vt, HEADS * mp * HDIM * 2);
-    ensure(rk, (size_t)n_layers * HEADS * pp * HDIM * 2);
+    ensure_pos(pl.tc);
+    {  // relative keys of every position of the table (encoder_blocks)
+      const void* old = rk.p;
+      ensure(rk, (size_t)n_layers * HEADS * round_up(2 * pos_t - 1, 64) * HDIM * 2);
+      if (rk.p != old) relk_t = 0;
+    }
     ensure(ao, mp * HIDDEN * 2);
     ensure(h, mp * HIDDEN * 4);
     ensure(h2, mp * HIDDEN * 4);
@@ -781,7 +788,6 @@ struct BarkHip {
       ensure(attn_po, tl.size() * HEADS * attention_query_tile() * HDIM * 2);
       ensure(attn_pml, tl.size() * HEADS * attention_query_tile() * 2 * 4);
     }
-    ensure_pos(pl.tc);
   }
 
   // Attention work list. Per sequence, its query tile x key tile units (in
@@ -939,7 +945,6 @@ struct BarkHip {
   // The blocks + projector over the packed rows in sub16 (pooler rows out).
   void encoder_blocks(const Plan& pl, int dump_layer, hipStream_t st) {
     const int mp = pl.mp, tc = pl.tc, prows = 2 * tc - 1;
-    const int pp = round_up(prows, 64);
     int mr = 0;  // real frames (algorithmic work excludes alignment rows)
     double attn_flops = 0;
     for (const auto& q : pl.seqs) {
@@ -957,12 +962,22 @@ struct BarkHip {
     es.bias = sub_b;
     gemm_op("sub_linear", sub16.as<half>(), 4096, mp, mr, sub_w, Epi::StoreF32, es, 4.0 * HIDDEN, st);
 
-    const half* pos_rows = pos.as<half>() + (size_t)(pos_t - tc) * HIDDEN;
-    {  // position keys of all layers: rk[l][h][r][d]
+    // Relative keys rk[l][h][r][d] = (pos[r] . W_relk[l]^T) for every row r of
+    // the position table (positions pos_t-1 .. -(pos_t-1)): they depend on the
+    // weights and the table only, so one GEMM per new table length serves
+    // every later encode; a sequence set whose longest length is tc reads the
+    // rows of positions tc-1 .. -(tc-1), which start at row pos_t - tc. A
+    // recomputation changes the offsets a captured graph holds, so it counts
+    // as a workspace change (ws_gen).
+    const int ppa = round_up(2 * pos_t - 1, 64);  // rk rows per head
+    if (relk_t != pos_t) {
       EpiArgs e;
       e.rk = rk.as<half>();
-      e.pp = pp;
-      gemm_op("relk", pos_rows, HIDDEN, prows, prows, relk_all, Epi::RelK, e, 2.0 * HIDDEN * n_layers, st);
+      e.pp = ppa;
+      const int rows = 2 * pos_t - 1;
+      gemm_op("relk", pos.as<half>(), HIDDEN, rows, rows, relk_all, Epi::RelK, e, 2.0 * HIDDEN * n_layers, st);
+      relk_t = pos_t;
+      ++ws_gen;
     }
     for (int l = 0; l < n_layers; ++l) {
       const DevLayer& L = layers[l];
@@ -989,8 +1004,8 @@ struct BarkHip {
       e.scale = attention_q_scale();
       gemm_op("qkv_heads", xnp, HIDDEN, mp, mr, L.qkv, Epi::Qkv, e, 2.0 * 4096, st);
       AttnArgs aa{qu.as<half>(), qv.as<half>(), kh.as<half>(), vt.as<half>(),
-                  rk.as<half>() + (size_t)l * HEADS * pp * HDIM,
-                  ao.as<half>(), mp, pp, tc, tiles.as<int4>(), ntiles, attn_lanes.as<int>(), nlanes,
+                  rk.as<half>() + ((size_t)l * HEADS * ppa + (size_t)(pos_t - tc)) * HDIM,
+                  ao.as<half>(), mp, ppa, tc, tiles.as<int4>(), ntiles, attn_lanes.as<int>(), nlanes,
                   attn_po.as<half>(), attn_pml.as<float>(), merges.as<int4>(), nmerges};
       prof.run("rel_attention", attn_flops, 2.0 * mr * HIDDEN * 5 + 2.0 * prows * HIDDEN, st,
                [&] { rel_attention(aa, st); });

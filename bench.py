@@ -593,7 +593,10 @@ def main() -> int:
         "dtype": "f16",
         "data": "synthetic (seeded log-mel N(0,1); random-init weights, 4-bit codes U{0..15} + sorted N(0,0.02) f16 tables)",
         "config": {"workload": "BASELINE configs[3]: 24-block 4-bit encoder, log-mel 17656x128 -> T=2207, batch 1",
-                   "frames": FRAMES, "T": T, "audio_s": AUDIO_S, "encoder_frames_per_s": T / dt},
+                   "frames": FRAMES, "T": T, "audio_s": AUDIO_S, "encoder_frames_per_s": T / dt,
+                   "relative_keys": "every layer's relK (position table x relative_k_proj) is computed when "
+                                    "the position table grows (the first encode of a new maximum length, "
+                                    "in warmup here) and read by later encodes"},
         "roofline": {"kernel": dom, "bound": "mfma" if mfma_bound else "hbm", "achieved": achieved, "peak": peak,
                      "unit": unit, "frac": achieved / peak, "traffic": traffic,
                      ("flops_per_launch" if mfma_bound else "bytes_per_launch"): per_launch,

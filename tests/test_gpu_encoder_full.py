@@ -208,6 +208,29 @@ def test_short_inputs_equal_their_batched_rows(pkg, synth):
             assert np.array_equal(b, s)
 
 
+def test_relk_table_growth_keeps_results(pkg, synth):
+    """The relative keys of every layer are computed once per position-table
+    length and kept: a longer input grows the table and recomputes them (and
+    retires graphs captured before), shorter inputs read a sub-range. Each
+    encode equals the same encode on a fresh handle, bit for bit, through
+    graph replays before and after the growth."""
+    src = synth.SynthCheckpoint(seed=47, n_layers=2, style="rich", lowbit=True)
+    fa, fb = 1500, 6000  # T = 188, then T = 750 (table 256 -> 750 rows)
+    ma, mb = synth.mel(fa, seed=5), synth.mel(fb, seed=6)
+    print(f"case relK table growth frames={fa},{fb}", flush=True)
+    with pkg.HipEncoder.load_with(src, n_layers=2) as fresh:
+        want_a = fresh.encode_mel(ma)[0]
+    with pkg.HipEncoder.load_with(src, n_layers=2) as fresh:
+        want_b = fresh.encode_mel(mb)[0]
+    with pkg.HipEncoder.load_with(src, n_layers=2) as enc:
+        for i in range(3):  # eager, capture, replay
+            assert np.array_equal(enc.encode_mel(ma)[0], want_a), f"short input, call {i}"
+        assert np.array_equal(enc.encode_mel(mb)[0], want_b), "longer input (table grows)"
+        for i in range(4):
+            assert np.array_equal(enc.encode_mel(ma)[0], want_a), f"short input after growth, call {i}"
+        assert np.array_equal(enc.encode_mel(mb)[0], want_b), "longer input again"
+
+
 def test_n_valid_masks_front_end(pkg, synth, oracle):
     """n_valid < n_frames zeroes the masked frames after each strided conv
     (src/sub.rs:259-273)."""
