@@ -843,8 +843,8 @@ __global__ void __launch_bounds__(512) gemm_strip_kernel(GemmParams p) {
   const int af_off = (32 * wid + l32) * LDK + 32 * lhi;  // this lane's A fragments
   // weight data of the fragments this wave makes: fragment f = wid + MW * i
   // is column block j = f / 4, slice s = f % 4 of every k-tile
-  // (the slice is a runtime value, so its code word is addressed in the load:
-  // picking a word of a loaded vector by a runtime index goes through scratch)
+  // (the slice depends on the wave, a runtime value, so the load addresses its
+  // code word directly: one 4-byte load, no runtime pick of a vector element)
   RowLut lut[FPW];
   const uint8_t* wsrc[FPW];
 #pragma unroll
