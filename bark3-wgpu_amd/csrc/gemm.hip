@@ -58,16 +58,26 @@ __device__ inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
 }
 
 // Row table as byte planes: L[q] holds the low bytes of entries 4q..4q+3,
-// H[q] the high bytes.
+// H[q] the high bytes. c4 is the constant 0x04040404; with OPQ it sits in a
+// vector register (opaque to the compiler), so the select mask of lookup4 is
+// one v_and_or_b32 (gfx950's three-operand encoding takes no 32-bit literal,
+// and with two literals the compiler splits it into an AND and an OR): 23
+// VALU instructions per 8 weights instead of 25, for one register, which
+// kernels at the register limit do without (OPQ = false).
 struct RowLut {
   uint32_t L[4], H[4];
+  uint32_t c4;
 };
 
+template <bool OPQ = true>
 __device__ inline RowLut load_row_lut(const half* lut_row) {
   const uint4 a = *reinterpret_cast<const uint4*>(lut_row);
   const uint4 b = *reinterpret_cast<const uint4*>(lut_row + 8);
   const uint32_t d[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
   RowLut t;
+  uint32_t c4 = 0x04040404u;
+  if constexpr (OPQ) asm volatile("" : "+v"(c4));
+  t.c4 = c4;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     t.L[q] = perm(d[2 * q + 1], d[2 * q], 0x06040200u);
@@ -82,7 +92,7 @@ __device__ inline void lookup4(uint32_t x, const RowLut& t, uint32_t& lo, uint32
   const uint32_t s7 = x & 0x07070707u;
   const uint32_t la = perm(t.L[1], t.L[0], s7), lb = perm(t.L[3], t.L[2], s7);
   const uint32_t ha = perm(t.H[1], t.H[0], s7), hb = perm(t.H[3], t.H[2], s7);
-  const uint32_t ms = ((x >> 1) & 0x04040404u) | 0x03020100u;  // byte i: i, or i+4 if code >= 8
+  const uint32_t ms = ((x >> 1) & t.c4) | 0x03020100u;  // byte i: i, or i+4 if code >= 8
   lo = perm(lb, la, ms);
   hi = perm(hb, ha, ms);
 }
@@ -615,7 +625,7 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4 && NB == 2) ? 2 : 1)
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int n = nw + 32 * j + l32;
-    if constexpr (LUT4) lut[j] = load_row_lut(p.lut + (size_t)n * 16);
+    if constexpr (LUT4) lut[j] = load_row_lut<!OCC2>(p.lut + (size_t)n * 16);
     boff[j] = (uint32_t)n * (uint32_t)(p.K / 2 * B_ROW_BYTES_PER_K2) + (LUT4 ? 16 : 64) * lhi;
   }
   constexpr int B_TILE_BYTES = LUT4 ? BK / 2 : BK * 2;
@@ -1187,7 +1197,7 @@ __global__ void __launch_bounds__(512, 1) gemm_k2_kernel(GemmParams p) {
   RowLut lut[2];
   if constexpr (LUT4) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) lut[j] = load_row_lut(p.lut + (size_t)(nw + 32 * j + l32) * 16);
+    for (int j = 0; j < 2; ++j) lut[j] = load_row_lut<false>(p.lut + (size_t)(nw + 32 * j + l32) * 16);
   }
   wait_vmcnt_le<0>();
 
