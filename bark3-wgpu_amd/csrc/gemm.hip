@@ -1197,7 +1197,8 @@ __global__ void __launch_bounds__(512, 1) gemm_k2_kernel(GemmParams p) {
   RowLut lut[2];
   if constexpr (LUT4) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) lut[j] = load_row_lut<false>(p.lut + (size_t)(nw + 32 * j + l32) * 16);
+    for (int j = 0; j < 2; ++j)  // the register form where it does not spill (SiLU)
+      lut[j] = load_row_lut<EPI == (int)Epi::Silu>(p.lut + (size_t)(nw + 32 * j + l32) * 16);
   }
   wait_vmcnt_le<0>();
 
