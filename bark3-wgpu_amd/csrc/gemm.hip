@@ -625,7 +625,9 @@ __global__ void __launch_bounds__(64 * WV, (LUT4 && FM <= 4 && NB == 2) ? 2 : 1)
 #pragma unroll
   for (int j = 0; j < NB; ++j) {
     const int n = nw + 32 * j + l32;
-    if constexpr (LUT4) lut[j] = load_row_lut<!OCC2>(p.lut + (size_t)n * 16);
+    // the register-held select mask except where it spills (two workgroups
+    // per CU at 128 rows with the f32 partial-sum store)
+    if constexpr (LUT4) lut[j] = load_row_lut<!(OCC2 && FM >= 4 && EPI == (int)Epi::StoreF32)>(p.lut + (size_t)n * 16);
     boff[j] = (uint32_t)n * (uint32_t)(p.K / 2 * B_ROW_BYTES_PER_K2) + (LUT4 ? 16 : 64) * lhi;
   }
   constexpr int B_TILE_BYTES = LUT4 ? BK / 2 : BK * 2;
