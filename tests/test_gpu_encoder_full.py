@@ -260,10 +260,13 @@ def test_long_stream_one_block(pkg, synth, oracle, t):
     assert e_blk <= TOL and e_pool <= TOL
 
 
-def test_reference_lowbit_format_equals_f16(pkg, synth):
+@pytest.mark.parametrize("t", [200, 1500])
+def test_reference_lowbit_format_equals_f16(pkg, synth, t):
     """The reference's LowBitTensor path (codes in 0..2k, k levels per row)
     gives bit-identical results to f16 weights holding the expanded values —
-    the invariant of the reference's `lbtest` (src/diagnostics/gemm.rs:538-652)."""
+    the invariant of the reference's `lbtest` (src/diagnostics/gemm.rs:538-652).
+    T = 200 runs the short-input strip tiles, T = 1500 the eight-wave tiles
+    (qkv, FFN down) and the four-wave ones."""
     low = synth.SynthCheckpoint(seed=71, n_layers=1, style="rich", lowbit=True, lowbit_format="levels", k_lev=3)
 
     class Expanded:
@@ -274,9 +277,10 @@ def test_reference_lowbit_format_equals_f16(pkg, synth):
         def read_lowbit(self, name):
             return None
 
-    sub = np.random.default_rng(71).standard_normal((200, 4096), dtype=np.float32)
+    print(f"case lbtest invariant T={t}", flush=True)
+    sub = np.random.default_rng(71).standard_normal((t, 4096), dtype=np.float32)
     with pkg.HipEncoder.load_with(low, n_layers=1, front_end=False) as a:
-        ya = a.encode(sub, 200, dump_layer=0)
+        ya = a.encode(sub, t, dump_layer=0)
     with pkg.HipEncoder.load_with(Expanded(), n_layers=1, front_end=False) as b:
-        yb = b.encode(sub, 200, dump_layer=0)
+        yb = b.encode(sub, t, dump_layer=0)
     assert np.array_equal(ya.pooler, yb.pooler) and np.array_equal(ya.block, yb.block)
