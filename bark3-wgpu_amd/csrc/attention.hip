@@ -627,13 +627,15 @@ __global__ void __launch_bounds__(NTW) rel_attn_wide_kernel(AttnArgs a) {
         (rho + e_lane < 32 ? b : j)[rho] = x[v];
       }
     };
+    // (the same condition as write_lower with the operands swapped: the two
+    // share one set of 16 lane masks, which otherwise fill 64 SGPRs)
     auto write_upper = [&](const floatx16& x) {
       lds_float *b = pl - 32, *j = pj;
       asm volatile("" : "+v"(b), "+v"(j));
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int rho = 8 * (v >> 2) + (v & 3);
-        (rho + e_lane >= 32 ? b : j)[rho] = x[v];
+        (rho + e_lane < 32 ? j : b)[rho] = x[v];
       }
     };
     auto wave_sync = [] {
