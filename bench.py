@@ -77,8 +77,10 @@ def bench_encoder(pkg, synth, torch, steps: int, warmup: int):
     src = synth.SynthCheckpoint(seed=0, n_layers=24, style="baseline", lowbit=True)
     t0 = time.time()
     # the decoder's weights ride along for the wave -> tokens pipeline measured
-    # after the encoder (they do not touch the encoder step)
-    enc = pkg.HipEncoder.load_with(src, device=0, n_layers=24, decoder=synth.SynthTdt(seed=0))
+    # after the encoder (they do not touch the encoder step); the blank row's
+    # bias is lowered so that the synthetic encoder's small outputs decode to a
+    # mix of token and blank steps (with the default bias every step is blank)
+    enc = pkg.HipEncoder.load_with(src, device=0, n_layers=24, decoder=synth.SynthTdt(seed=0, blank_bias=-1.0))
     log(f"[bench] weights loaded in {time.time() - t0:.1f}s")
     mel = torch.from_numpy(synth.mel(FRAMES, seed=0)).cuda()
     T = pkg.conv_len(pkg.conv_len(pkg.conv_len(FRAMES)))
@@ -131,7 +133,8 @@ def bench_pipeline(enc, reps: int = 3):
     """bark_hip_transcribe_wave_batch on the workload's 176.56 s wave from host
     memory: upload, log-mel, the 24-block encoder and the greedy TDT decode of
     the pooler in device memory, tokens back to the host. The synthetic
-    encoder's outputs are small, so the decoder's biases decide its steps."""
+    encoder's outputs are small, so the decoder's biases decide its steps
+    (the blank bias is set for a mix of token and blank steps)."""
     enc.set_mel_filters()
     wave = mel_wave()
     toks = enc.transcribe_wave_batch([wave])[0]
