@@ -150,6 +150,10 @@ def bench_pipeline(enc, reps: int = 3):
             "includes": "host->device wave upload (11.3 MB), log-mel, 24-block encoder, TDT decode, tokens to host"}
 
 
+# the isolated 4-bit linear's (T, K, N) shapes
+GEMM_SHAPES = [(t, k, n) for t in (188, 2207) for k, n in ((1024, 4096), (4096, 1024), (1024, 3072))]
+
+
 def bench_gemm(pkg, torch, T: int, K: int, N: int, reps: int = 192):
     """Average launch time of the isolated 4-bit linear over `reps` distinct
     buffer sets (codes + activations + outputs)."""
@@ -448,13 +452,9 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def traffic_workload(pkg, synth, torch, t: int = 2207, f16: bool = False) -> None:
-    """What the counter passes profile (rocprofv3 --pmc ... -- python3 bench.py
-    --traffic-workload [--traffic-t T] [--traffic-f16]): a 512 MiB device copy
-    whose bytes calibrate the traffic counters, then two encodes of a 1-block
-    encoder (4-bit, or f16 weights) on a synthetic log-mel giving T encoder
-    frames: front end, one block and projector, the per-layer launches of the
-    24-block step."""
+def calibration_copy(torch) -> None:
+    """A 512 MiB device-to-device copy: the counter passes scale FETCH_SIZE and
+    WRITE_SIZE by what they read for its known bytes."""
     a = torch.empty(128 << 20, dtype=torch.float32, device="cuda")
     a.fill_(1.0)
     b = torch.empty_like(a)
@@ -462,6 +462,28 @@ def traffic_workload(pkg, synth, torch, t: int = 2207, f16: bool = False) -> Non
     b.copy_(a)
     torch.cuda.synchronize()
     del a, b
+    torch.cuda.empty_cache()
+
+
+def gemm_workload(pkg, torch) -> None:
+    """What the isolated-linear counter passes profile (rocprofv3 ... -- python3
+    bench.py --gemm-workload): the calibration copy, then bench_gemm over the
+    six configs[1] shapes in order, each launched 2 x 192 times over 192
+    distinct buffer sets (warm-up pass, then the timed pass)."""
+    calibration_copy(torch)
+    for t, k, n in GEMM_SHAPES:
+        r = bench_gemm(pkg, torch, t, k, n)
+        log(f"[bench] lowbit linear T={t} K={k} N={n}: {r['us']:.2f} us")
+
+
+def traffic_workload(pkg, synth, torch, t: int = 2207, f16: bool = False) -> None:
+    """What the counter passes profile (rocprofv3 --pmc ... -- python3 bench.py
+    --traffic-workload [--traffic-t T] [--traffic-f16]): a 512 MiB device copy
+    whose bytes calibrate the traffic counters, then two encodes of a 1-block
+    encoder (4-bit, or f16 weights) on a synthetic log-mel giving T encoder
+    frames: front end, one block and projector, the per-layer launches of the
+    24-block step."""
+    calibration_copy(torch)
     frames = 8 * t
     while pkg.conv_len(pkg.conv_len(pkg.conv_len(frames))) > t:
         frames -= 1
@@ -488,6 +510,8 @@ def main() -> int:
                     help="run only the workload of the counter passes")
     ap.add_argument("--traffic-t", type=int, default=2207, help="encoder frames of the counter workload")
     ap.add_argument("--traffic-f16", action="store_true", help="counter workload with f16 weights")
+    ap.add_argument("--gemm-workload", action="store_true",
+                    help="run only the isolated 4-bit linear's counter workload")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -504,6 +528,9 @@ def main() -> int:
 
     if args.traffic_workload:
         traffic_workload(pkg, synth, torch, args.traffic_t, args.traffic_f16)
+        return 0
+    if args.gemm_workload:
+        gemm_workload(pkg, torch)
         return 0
 
     enc, dt, T, prof, dom, d, pipe = bench_encoder(pkg, synth, torch, args.steps, args.warmup)
@@ -555,12 +582,11 @@ def main() -> int:
 
     gemm = []
     if not args.no_gemm:
-        for t in (188, 2207):
-            for k, n in ((1024, 4096), (4096, 1024), (1024, 3072)):
-                r = bench_gemm(pkg, torch, t, k, n)
-                gemm.append(r)
-                log(f"[bench] lowbit linear T={t} K={k} N={n}: {r['us']:.2f} us, {r['tflops']:.1f} TFLOP/s, "
-                    f"{r['gbs']:.0f} GB/s")
+        for t, k, n in GEMM_SHAPES:
+            r = bench_gemm(pkg, torch, t, k, n)
+            gemm.append(r)
+            log(f"[bench] lowbit linear T={t} K={k} N={n}: {r['us']:.2f} us, {r['tflops']:.1f} TFLOP/s, "
+                f"{r['gbs']:.0f} GB/s")
 
     mel = bench_mel(pkg, torch)
     log(f"[bench] log-mel front end: {mel['gpu_ms']:.3f} ms for {mel['audio_s']:.2f} s of audio "
