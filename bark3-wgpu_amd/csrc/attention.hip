@@ -587,22 +587,26 @@ __global__ void __launch_bounds__(NTW) rel_attn_wide_kernel(AttnArgs a) {
     };
 
     // ---- segment prologue (all 512 threads): the ring's first ten blocks and
-    // the first tile's K and V^T
+    // the first tile's K and V^T. Every load is issued before the first LDS
+    // store, so the prologue waits for memory once (a load-store loop waited
+    // once per pair of ring chunks).
     {
       const int col16 = (tid & 15) * 8, row32 = tid >> 4;
-#pragma unroll 2
-      for (int i = 0; i < RW_CH; ++i)
-        *reinterpret_cast<uint4*>(&sm.R[(32 * i + row32) * KLD + col16]) =
-            *reinterpret_cast<const uint4*>(rk_row(i, row32) + col16);
+      const int vd = tid >> 3, kc = (tid & 7) * 8;
+      uint4 pr[RW_CH], pk[KW_CH], pv[VW_CH];
+#pragma unroll
+      for (int i = 0; i < RW_CH; ++i) pr[i] = *reinterpret_cast<const uint4*>(rk_row(i, row32) + col16);
 #pragma unroll
       for (int i = 0; i < KW_CH; ++i)
-        *reinterpret_cast<uint4*>(&sm.K[(row32 + 32 * i) * KLD + col16]) =
-            ld_u4(kbase + (size_t)k_begin * HDIM, (uint32_t)((row32 + 32 * i) * HDIM + col16) * 2u);
-      const int vd = tid >> 3, kc = (tid & 7) * 8;
+        pk[i] = ld_u4(kbase + (size_t)k_begin * HDIM, (uint32_t)((row32 + 32 * i) * HDIM + col16) * 2u);
 #pragma unroll
-      for (int i = 0; i < VW_CH; ++i)
-        stage_vt(sm.V, vd + 64 * i, kc, ld_u4(vbase + k_begin, (uint32_t)((vd + 64 * i) * a.mp + kc) * 2u),
-                 T - (k_begin + kc));
+      for (int i = 0; i < VW_CH; ++i) pv[i] = ld_u4(vbase + k_begin, (uint32_t)((vd + 64 * i) * a.mp + kc) * 2u);
+#pragma unroll
+      for (int i = 0; i < RW_CH; ++i) *reinterpret_cast<uint4*>(&sm.R[(32 * i + row32) * KLD + col16]) = pr[i];
+#pragma unroll
+      for (int i = 0; i < KW_CH; ++i) *reinterpret_cast<uint4*>(&sm.K[(row32 + 32 * i) * KLD + col16]) = pk[i];
+#pragma unroll
+      for (int i = 0; i < VW_CH; ++i) stage_vt(sm.V, vd + 64 * i, kc, pv[i], T - (k_begin + kc));
     }
     __syncthreads();
 
