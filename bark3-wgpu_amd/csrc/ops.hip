@@ -274,11 +274,20 @@ __global__ void __launch_bounds__(256) conv1_dw_kernel(const float* mel, int fra
   const int tid = threadIdx.x;
   const int ii0 = 2 * r0 - 1;           // first conv1 row
   const int mr0 = 2 * ii0 - 1;          // first mel row
-  for (int i = tid; i < FD_MELR * (MEL + 2); i += 256) {
+  // every load of the patch is issued before its first LDS store (one wait
+  // for memory, not one per element)
+  constexpr int PATCH_N = FD_MELR * (MEL + 2), PATCH_IT = (PATCH_N + 255) / 256;
+  float pv[PATCH_IT];
+#pragma unroll
+  for (int k = 0; k < PATCH_IT; ++k) {
+    const int i = tid + 256 * k;
     const int r = i / (MEL + 2), ci = i % (MEL + 2);
     const int si = mr0 + r, sj = ci - 1;
-    patch[r][ci] = (si >= 0 && si < frames && sj >= 0 && sj < MEL) ? mel[(size_t)si * MEL + sj] : 0.0f;
+    pv[k] = (i < PATCH_N && si >= 0 && si < frames && sj >= 0 && sj < MEL) ? mel[(size_t)si * MEL + sj] : 0.0f;
   }
+#pragma unroll
+  for (int k = 0; k < PATCH_IT; ++k)
+    if (tid + 256 * k < PATCH_N) (&patch[0][0])[tid + 256 * k] = pv[k];
   __syncthreads();
   const int cg = tid & 7, pg = tid >> 3;  // channel group (4 channels), position group
   const int cl = 4 * cg, c = blockIdx.y * FD_CH + cl;
