@@ -373,21 +373,24 @@ __global__ void __launch_bounds__(256) sub_dw_kernel(const half* in, int t_in, i
     const int pix = blockIdx.x * DW2_PIX + p;
     if (pix >= npix) break;
     const int i = pix / m_out, j = pix % m_out;
+    // the nine taps' loads first (one wait for memory), then the sum over the
+    // in-range taps in (ki, kj) order
+    half8 xt[9];
+    bool ok[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) {
+      const int ii = 2 * i + t / 3 - 1, jj = 2 * j + t % 3 - 1;
+      ok[t] = ii >= 0 && ii < t_in && jj >= 0 && jj < m_in;
+      xt[t] = ok[t] ? ld_half8(in + ((size_t)ii * m_in + jj) * SUB_CH + c) : half8{};
+    }
     float s[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) s[e] = bias[e];
 #pragma unroll
-    for (int ki = 0; ki < 3; ++ki) {
-      const int ii = 2 * i + ki - 1;
-      if (ii < 0 || ii >= t_in) continue;
+    for (int t = 0; t < 9; ++t) {
+      if (!ok[t]) continue;
 #pragma unroll
-      for (int kj = 0; kj < 3; ++kj) {
-        const int jj = 2 * j + kj - 1;
-        if (jj < 0 || jj >= m_in) continue;
-        const half8 x = ld_half8(in + ((size_t)ii * m_in + jj) * SUB_CH + c);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s[e] = fmaf(wr[e][ki * 3 + kj], (float)x[e], s[e]);
-      }
+      for (int e = 0; e < 8; ++e) s[e] = fmaf(wr[e][t], (float)xt[t][e], s[e]);
     }
     half8 z;
 #pragma unroll
